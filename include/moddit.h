@@ -1,0 +1,190 @@
+/*
+ * moddit.h — C ABI of the MI355X (gfx950) MOD-DiT sparse-attention hot path.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, sizes and element strides (no framework types);
+ *   - launches on the caller's HIP stream (passed as an opaque pointer, NULL means
+ *     the null stream) and never synchronises the device;
+ *   - returns MODDIT_OK (0) or a nonzero status; moddit_last_error() then returns a
+ *     thread-local message describing the failure;
+ *   - writes only into caller-allocated outputs, except where a workspace is named.
+ *
+ * Element strides are in elements, not bytes. Attention tensors are addressed as
+ * [batch][head][token][dim] with an arbitrary (batch, head, token) stride triple and a
+ * unit dim stride, which covers both contiguous (B,H,S,D) tensors and (B,S,H,D)
+ * storage viewed as (B,H,S,D).
+ *
+ * Each declaration names the reference interface it replaces (path:line inside the
+ * MOD-DiT source tree).
+ */
+#ifndef MODDIT_H_
+#define MODDIT_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* moddit_stream_t; /* a hipStream_t */
+
+enum moddit_status {
+  MODDIT_OK = 0,
+  MODDIT_EINVAL = 1,      /* invalid argument (shape, stride, alignment, range) */
+  MODDIT_EUNSUPPORTED = 2,/* valid but unsupported combination (dtype, head_dim)   */
+  MODDIT_EHIP = 3         /* a HIP runtime call failed                            */
+};
+
+enum moddit_dtype { MODDIT_BF16 = 0, MODDIT_FP16 = 1, MODDIT_FP32 = 2 };
+
+/* Per-head mask mode, the reference's 'sparse' / 'block_diagonal' / 'full' strings. */
+enum moddit_head_mode { MODDIT_MODE_SPARSE = 0, MODDIT_MODE_BLOCK_DIAGONAL = 1, MODDIT_MODE_FULL = 2 };
+
+/* Token layouts of MoD/mod/triton_flash_sparsity.py:101-120 and attn_mask.py:541-557. */
+enum moddit_layout { MODDIT_LAYOUT_WAN = 0, MODDIT_LAYOUT_HUNYUAN = 1, MODDIT_LAYOUT_COGVIDEOX = 2, MODDIT_LAYOUT_OTHER = 3 };
+
+/* Thread-local text of the last failure on this thread ("" if none). */
+const char* moddit_last_error(void);
+
+/* Library version string. */
+const char* moddit_version(void);
+
+/*
+ * Dense attention forward with a natural-log LSE output.
+ *   O[b,h,r,:] = softmax_r(scale * Q[b,h,r,:] . K[b,h,c,:]) over c < kv_len, then . V
+ *   LSE[b,h,r] = log(sum_c exp(scale * q.k))   (fp32, contiguous (B,H,S); may be NULL)
+ * q/k/v/o: dtype elements, head_dim D in {64,128}; q_len rows of Q/O, kv_len rows of K/V.
+ * Replaces flash_attn_func (MoD/mod/triton_flash_sparsity.py:320-321), sageattn
+ * (MoD/mod/attn_mask.py:271-276), flashinfer.single_prefill_with_kv_cache
+ * (attn_mask.py:283-289) and the processors' F.scaled_dot_product_attention
+ * (MoD/models/hunyuan/attention_processor.py:122-124).
+ */
+int moddit_flash_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                     int batch, int heads, int q_len, int kv_len, int head_dim,
+                     const int64_t q_strides[3], const int64_t k_strides[3],
+                     const int64_t v_strides[3], const int64_t o_strides[3],
+                     float softmax_scale, int dtype, moddit_stream_t stream);
+
+/*
+ * Block-sparse attention forward. Query rows are grouped in tiles of 128 (two
+ * 64-row query blocks) and keys in tiles of 64. For head h and query tile t the
+ * active key tiles are entries[(h*n_qtiles + t)*cap + i], i < counts[h*n_qtiles + t],
+ * in ascending order, each encoded as (key_tile << 2) | rows, where bit 0 enables
+ * the tile for query rows 0..63 of the query tile and bit 1 for rows 64..127.
+ * Rows with no active key tile produce zeros and LSE = -inf.
+ * Replaces block_sparse_sage2_attn_cuda (MoD/mod/attn_mask.py:306,312-317) as driven
+ * by AttentionSparseEngine (attn_mask.py:266-331).
+ */
+int moddit_block_sparse_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                            int batch, int heads, int q_len, int kv_len, int head_dim,
+                            const int64_t q_strides[3], const int64_t k_strides[3],
+                            const int64_t v_strides[3], const int64_t o_strides[3],
+                            float softmax_scale, int dtype,
+                            const int32_t* counts, const int32_t* entries, int n_qtiles, int cap,
+                            moddit_stream_t stream);
+
+/*
+ * Replayed block sparsity map (video x video blocks), fp16 output (B,H,n,n):
+ *   map[b,h,i,j] = fp16_rn( #{(r,c) in block (i,j) :
+ *                   fp32(sum_d round(q[r,d]*scale) * k[c,d]) < lse[r] + log_threshold}
+ *                   / block_size^2 )
+ * where round() is round-to-nearest-even to the input dtype and r, c are offset by
+ * q_video_offset / k_video_offset. log_threshold = -inf gives an all-zero map.
+ * lse: fp32 contiguous (B,H,S). block_size in {64,128}.
+ * Replaces the pybind `sparsity_map` (MoD/mod/cuda_flash_sparsity_kernel.cu:289-334)
+ * and the Triton `_sparsity_kernel` (MoD/mod/triton_flash_sparsity.py:28-98).
+ */
+int moddit_sparsity_map(const void* q, const void* k, const float* lse, void* map_out,
+                        int batch, int heads, int seq_len, int head_dim,
+                        const int64_t q_strides[3], const int64_t k_strides[3],
+                        float softmax_scale, float log_threshold,
+                        int q_video_offset, int k_video_offset, int video_blocks, int block_size,
+                        int dtype, moddit_stream_t stream);
+
+/*
+ * M^T S for the line model, per head (H, 3n) fp32:
+ *   [0, 2n-1)   diagonal sums, index k <-> offset k-(n-1) (col - row)
+ *   [2n-1, 3n-1) column sums
+ *   3n-1        sum over the n/bpf frame-diagonal bpf x bpf blocks
+ * map: contiguous (H,n,n) of map_dtype (FP16: summed exactly in 2^-24 fixed point and
+ * rounded once to fp32; FP32: summed in fp64 and rounded once).
+ * Replaces compute_mts (MoD/mod/cuda_lstsq_kernel.cu:421-482, kernels :17-162).
+ */
+int moddit_mts(const void* map, int map_dtype, int heads, int n, int blocks_per_frame,
+               float* mts_out, moddit_stream_t stream);
+
+/*
+ * Closed-form M^T M + lambda*I (F = 3n) written as doubles into a HOST buffer of F*F.
+ * Replaces compute_mtm (MoD/mod/cuda_lstsq_kernel.cu:319-418; torch twin
+ * MoD/mod/cuda_lstsq.py:42-89).
+ */
+int moddit_mtm_host(int n, int blocks_per_frame, double regularization, double* mtm_out);
+
+/*
+ * X[h,:] = Ginv . mts[h,:] for all heads: ginv (F,F) fp32 row-major (symmetric inverse of
+ * M^T M + lambda*I), mts (H,F), x (H,F).
+ * Replaces _solve_all_heads (MoD/mod/cuda_lstsq.py:189-208).
+ */
+int moddit_solve(const float* ginv, const float* mts, float* x, int heads, int features,
+                 moddit_stream_t stream);
+
+/*
+ * Line prediction and selection: with c = X[:,2n-1:3n-1]/2 and d = X[:,:2n-1] for the
+ * current (x_cur) and previous (x_last) fits, pred = cur + (cur - last) / predict_T over
+ * v = [pred_c (n), pred_d (2n-1)]; selects the k = min(top_k, 3n-1) smallest per head,
+ * ties broken by lower index, NaN ordered last. Writes the selected indices in ascending
+ * index order to sel_out (H,k) int32.
+ * Replaces choose_topk_lines (MoD/mod/attn_mask.py:351-370).
+ */
+int moddit_select_lines(const float* x_cur, const float* x_last, int heads, int n,
+                        int predict_T, int top_k, int32_t* sel_out, moddit_stream_t stream);
+
+/*
+ * Block-diagonal mode decision: for each head with mode[h] == SPARSE,
+ * mode[h] = BLOCK_DIAGONAL if x[h, features-1] <= threshold.
+ * Replaces check_bd_values (MoD/mod/attn_mask.py:336-349).
+ */
+int moddit_check_bd(const float* x, int heads, int features, float threshold, uint8_t* mode,
+                    moddit_stream_t stream);
+
+/*
+ * Block mask from selected lines and the attention kernel's tile lists.
+ *   video[h,i,j] = mode==FULL | col_sel[j] | diag_sel[j-i+n-1] | (mode==BD & i/bpf==j/bpf)
+ *   mask (H,nb,nb) bool (1 byte) merged per layout (wan: nb=n; hunyuan: video first,
+ *   text rows/cols true; cogvideox: text first; other: all true).
+ * counts/entries receive the tile lists of moddit_block_sparse_fwd for the mask at
+ * block_size granularity (64 or 128); union_rows=1 reproduces the reference engine's
+ * 128-row union (both row bits set whenever either 64-row block is active).
+ * mask_out, counts or entries may be NULL to skip that output.
+ * Replaces generate_mask_from_lines (MoD/mod/attn_mask.py:440-559) and the mask
+ * conversion of AttentionSparseEngine (attn_mask.py:296-304).
+ */
+int moddit_mask_from_lines(const int32_t* sel, int heads, int k, const uint8_t* mode,
+                           int n, int blocks_per_frame, int layout, int nb, int text_blocks,
+                           int block_size, int union_rows, uint8_t* mask_out,
+                           int32_t* counts, int32_t* entries, int n_qtiles, int cap,
+                           moddit_stream_t stream);
+
+/*
+ * Tile lists from an explicit bool block mask (H,nb,nb) at block_size granularity, the
+ * same encoding as moddit_mask_from_lines; key tiles at or beyond kv_tiles are dropped.
+ * Replaces the mask conversion of AttentionSparseEngine (MoD/mod/attn_mask.py:296-311).
+ */
+int moddit_mask_to_tiles(const uint8_t* mask, int heads, int nb, int block_size, int union_rows,
+                         int kv_tiles, int32_t* counts, int32_t* entries, int n_qtiles, int cap,
+                         moddit_stream_t stream);
+
+/*
+ * Refresh merge: out[h,i,j] = mask[h,i,j] ? cur[h,i,j] : prev[h,i,j] over (H,n,n) fp16,
+ * where mask is addressed as mask[h*mask_head_stride + i*mask_row_stride + j].
+ * out may alias prev. Replaces the torch.where of MoD/mod/attn_mask.py:671-675.
+ */
+int moddit_refresh_merge(const void* prev, const void* cur, const uint8_t* mask,
+                         int64_t mask_head_stride, int64_t mask_row_stride,
+                         int heads, int n, void* out, moddit_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MODDIT_H_ */

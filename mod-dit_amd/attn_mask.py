@@ -1,0 +1,364 @@
+"""MOD-DiT sparse-attention step machine on gfx950 (drop-in for MoD/mod/attn_mask.py).
+
+Public functions keep the reference's names, signatures and return values:
+  SparseAttentionWithMap (:567-729)   per-call warmup / predict / refresh / sparse machine
+  AttentionSparseEngine (:266-331)    dense or block-sparse attention from a block mask
+  update_warmup (:117-146), extract_attention_features (:76-115)
+  check_bd_values (:336-349), choose_topk_lines (:351-370)
+  predict_mask_from_warmup (:373-436), generate_mask_from_lines (:440-559)
+
+Differences that are deliberate:
+  * no host synchronisation on the path: head modes stay on the device (HeadModes
+    behaves like the reference's list of strings when read), the block-diagonal test,
+    line selection, mask construction and the refresh merge are device kernels, and the
+    engine never calls mask.all();
+  * selected lines come back in ascending index order (the reference's
+    topk(sorted=False) order is unspecified); ties at the k-th value go to the lower
+    index;
+  * the mask kernel also emits the attention tile lists, so sparse steps do not
+    convert the mask again;
+  * sparse types other than 'mod-dit' ('radial', 'spargeattn') and the Hunyuan text
+    tail of the sparse engine call third-party kernels in the reference and raise
+    NotImplementedError here.
+"""
+from __future__ import annotations
+
+import logging
+from collections.abc import Sequence
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+from . import _lib, ops
+from .flash_sparsity import flash_attn_with_sparsity_map
+from .lstsq import solve_lstsq
+from .state import is_warmup_complete
+
+_MODE_CODES = {"sparse": _lib.MODE_SPARSE, "block_diagonal": _lib.MODE_BLOCK_DIAGONAL,
+               "full": _lib.MODE_FULL}
+_MODE_NAMES = {v: k for k, v in _MODE_CODES.items()}
+_LAYOUTS = {"wan": _lib.LAYOUT_WAN, "hunyuan": _lib.LAYOUT_HUNYUAN,
+            "cogvideox": _lib.LAYOUT_COGVIDEOX}
+
+
+class HeadModes(Sequence):
+    """Per-head mask modes kept as a device uint8 tensor.
+
+    Reads like the reference's list of 'sparse' / 'block_diagonal' / 'full' strings; the
+    device-to-host copy happens only when an element is actually read.
+    """
+
+    def __init__(self, codes: torch.Tensor):
+        self.codes = codes
+        self._names: Optional[List[str]] = None
+
+    def _host(self) -> List[str]:
+        if self._names is None:
+            self._names = [_MODE_NAMES[int(c)] for c in self.codes.tolist()]
+        return self._names
+
+    def __len__(self):
+        return self.codes.shape[0]
+
+    def __getitem__(self, i):
+        return self._host()[i]
+
+    def __eq__(self, other):
+        return list(self) == list(other)
+
+    def __repr__(self):
+        return f"HeadModes({self._host()!r})"
+
+
+def _mode_tensor(mode, num_heads: int, device) -> torch.Tensor:
+    if isinstance(mode, HeadModes):
+        return mode.codes
+    if torch.is_tensor(mode):
+        return mode.to(device=device, dtype=torch.uint8)
+    codes = [_MODE_CODES.get(m, _lib.MODE_SPARSE) for m in list(mode)]
+    if len(codes) != num_heads:
+        raise ValueError(f"mode has {len(codes)} entries for {num_heads} heads")
+    return torch.tensor(codes, dtype=torch.uint8, device=device)
+
+
+# ======================================================================================
+# feature extraction / warmup bookkeeping
+# ======================================================================================
+def extract_attention_features(warmup_state: Dict, S_T: torch.Tensor, blocks_per_frame: int,
+                               layer_idx: int = 0, regularization: float = 1,
+                               use_cuda: bool = True) -> Dict[str, torch.Tensor]:
+    """Fit the line model to S_T (H, n, n); MoD/mod/attn_mask.py:76-115 (lambda = 1)."""
+    num_heads, n = S_T.shape[0], S_T.shape[1]
+    assert S_T.shape == (num_heads, n, n), f"S_T shape mismatch: {S_T.shape} vs ({num_heads}, {n}, {n})"
+    return solve_lstsq(warmup_state=warmup_state, S_T=S_T, step=warmup_state["current_steps"],
+                       layer_idx=layer_idx, blocks_per_frame=blocks_per_frame,
+                       regularization=regularization, use_cuda=use_cuda)
+
+
+def update_warmup(warmup_state: Dict, step: int, block_sparse_map: torch.Tensor):
+    """MoD/mod/attn_mask.py:117-146."""
+    if step == warmup_state["warmup_steps"] - 2:
+        warmup_state["features_history"] = []
+        warmup_state["current_steps"] = step
+        warmup_state["prev_full_maps"] = block_sparse_map
+    features = extract_attention_features(warmup_state=warmup_state, S_T=block_sparse_map,
+                                          blocks_per_frame=warmup_state["blocks_per_frame"],
+                                          use_cuda=warmup_state["use_cuda"])
+    warmup_state["features_history"].append(features)
+    warmup_state["current_steps"] = step + 1
+    warmup_state["prev_full_maps"] = block_sparse_map
+
+
+# ======================================================================================
+# mask prediction
+# ======================================================================================
+def check_bd_values(values: torch.Tensor, mode: List[str], threshold: float = -7.5e-2):
+    """Host-list form of MoD/mod/attn_mask.py:336-349 (reads `values` on the host).
+
+    The step machine uses the device kernel (ops.check_bd) instead.
+    """
+    last = values[:, -1].tolist()
+    for i in range(values.shape[0]):
+        if mode[i] == "sparse" and last[i] <= threshold:
+            mode[i] = "block_diagonal"
+    return mode
+
+
+def _x_of(features: Dict[str, torch.Tensor]) -> torch.Tensor:
+    x = features.get("_x")
+    if x is not None:
+        return x
+    d, c, b = features["d"], features["c"], features["b_d"]
+    return torch.cat([d, c * 2, b.reshape(-1, 1)], dim=1).to(torch.float32).contiguous()
+
+
+def _select_i32(history, top_k: int, predict_T) -> torch.Tensor:
+    x_last, x_cur = _x_of(history[-2]), _x_of(history[-1])
+    n = x_cur.shape[1] // 3
+    return ops.select_lines(x_cur, x_last, n, predict_T, top_k)
+
+
+def choose_topk_lines(history: List[Dict[str, torch.Tensor]], top_k: int = 10,
+                      predict_T: int = None) -> torch.Tensor:
+    """k smallest of cat(pred_c, pred_d) per head; MoD/mod/attn_mask.py:351-370.
+
+    Returns (H, k) int64 indices (index < n: column, else diagonal offset idx-n-(n-1)),
+    in ascending order.
+    """
+    return _select_i32(history, top_k, predict_T).long()
+
+
+def _generate_mask_and_tiles(warmup_state: Dict, num_heads: int, n: int, blocks_per_frame: int,
+                             selected_lines, mode, device, want_tiles=True):
+    block_size = warmup_state["block_size"]
+    block_num = n // block_size
+    text_block_num = warmup_state["text_token_num"] // block_size
+    video_block_num = warmup_state["video_token_num"] // block_size
+    model_type = warmup_state.get("model_type")
+    layout = _LAYOUTS.get(model_type, _lib.LAYOUT_OTHER)
+    if layout == _lib.LAYOUT_WAN:
+        nb = video_block_num
+    else:
+        nb = block_num
+    if layout == _lib.LAYOUT_COGVIDEOX and block_num - text_block_num != video_block_num:
+        raise RuntimeError(
+            f"cogvideox mask: {block_num - text_block_num} video blocks in the sequence "
+            f"but video_token_num gives {video_block_num}"
+        )
+    if layout == _lib.LAYOUT_HUNYUAN and block_num < video_block_num:
+        raise RuntimeError("hunyuan mask: video blocks exceed the sequence")
+    if not torch.is_tensor(selected_lines):
+        selected_lines = torch.as_tensor(selected_lines)
+    selected_lines = selected_lines.to(device=device)
+    if selected_lines.dim() == 1:
+        selected_lines = selected_lines.unsqueeze(1)
+    modes = _mode_tensor(mode, num_heads, device)
+    union = warmup_state.get("tile_rows", "union") == "union"
+    n_video = max(video_block_num, 1)
+    return ops.mask_from_lines(selected_lines, modes, n=n_video,
+                               blocks_per_frame=max(int(blocks_per_frame), 1), layout=layout,
+                               nb=nb, text_blocks=text_block_num, block_size=block_size,
+                               union_rows=union, want_mask=True, want_tiles=want_tiles)
+
+
+def generate_mask_from_lines(warmup_state: Dict, num_heads: int, n: int, blocks_per_frame: int,
+                             selected_lines, mode, device) -> torch.Tensor:
+    """Bool block mask from selected lines; MoD/mod/attn_mask.py:440-559."""
+    mask, _ = _generate_mask_and_tiles(warmup_state, num_heads, n, blocks_per_frame,
+                                       selected_lines, mode, device, want_tiles=False)
+    return mask
+
+
+def predict_mask_from_warmup(warmup_state: Dict, n: int, top_k: int = 10,
+                             layer_idx: int = 0) -> Dict:
+    """First mask after warmup; MoD/mod/attn_mask.py:373-436."""
+    num_heads = warmup_state["num_heads"]
+    blocks_per_frame = warmup_state["blocks_per_frame"]
+    if not is_warmup_complete(warmup_state):
+        device = torch.device("cuda") if torch.cuda.is_available() else torch.device("cpu")
+        nb = n // warmup_state["block_size"]
+        return {
+            "mode": ["full"] * num_heads,
+            "block_diagonal": [False] * num_heads,
+            "selected_lines": [],
+            "mask": torch.ones(num_heads, nb, nb, dtype=torch.bool, device=device),
+        }
+    history = warmup_state["features_history"]
+    x_cur = _x_of(history[-1])
+    device = x_cur.device
+    modes = torch.zeros(num_heads, dtype=torch.uint8, device=device)
+    ops.check_bd(x_cur, modes, threshold=1.0)
+    mode = HeadModes(modes)
+    selected = _select_i32(history, top_k, warmup_state.get("predict_T", None))
+    mask, tiles = _generate_mask_and_tiles(warmup_state, num_heads, n, blocks_per_frame,
+                                           selected, mode, device)
+    return {"mode": mode, "selected_lines": selected.long(), "mask": mask, "_tiles": tiles}
+
+
+# ======================================================================================
+# attention engine
+# ======================================================================================
+def _log_sparsity(logger, layer_idx: int, mask: torch.Tensor) -> None:
+    # The value needs a device read; only pay for it when the message is emitted.
+    if logger is not None and logger.isEnabledFor(logging.INFO):
+        logger.info(f"Layer {layer_idx}, Mask Sparsity: {1 - mask.float().mean():.3%}")
+
+
+def _kv_border(pre_defined_mask: torch.Tensor) -> int:
+    return int(pre_defined_mask[0].sum().item())
+
+
+def _engine(query, key, value, mask, tiles, pre_defined_mask, video_token_num, block_size,
+            union_rows):
+    if pre_defined_mask is not None:
+        raise NotImplementedError(
+            "AttentionSparseEngine: the text-token tail with pre_defined_mask (Hunyuan layout) "
+            "is not implemented in this build"
+        )
+    if mask.dim() == 2:
+        mask = mask.unsqueeze(0).expand(query.shape[1], -1, -1)
+    if tiles is None:
+        tiles = ops.mask_to_tiles(mask, block_size, union_rows=union_rows)
+    out, _ = ops.block_sparse_fwd(query, key, value, tiles)
+    return out
+
+
+def AttentionSparseEngine(query, key, value, mask, pre_defined_mask=None, video_token_num=0,
+                          block_size=128, union_rows: bool = True):
+    """Block-sparse attention under a bool block mask; MoD/mod/attn_mask.py:266-331.
+
+    union_rows=True executes each pair of 64-row mask rows as one 128-row query tile over
+    the union of their key blocks, which is what the reference engine runs (:299-303).
+    """
+    return _engine(query, key, value, mask, None, pre_defined_mask, video_token_num,
+                   block_size, union_rows)
+
+
+def _dense_engine(query, key, value, pre_defined_mask):
+    if pre_defined_mask is not None:
+        raise NotImplementedError(
+            "dense engine with pre_defined_mask (Hunyuan text tail) is not implemented in this build"
+        )
+    out, _ = ops.flash_fwd(query, key, value, return_lse=False)
+    return out
+
+
+# ======================================================================================
+# step machine
+# ======================================================================================
+def _video_part(warmup_state: Dict, mask: torch.Tensor) -> torch.Tensor:
+    bs = warmup_state["block_size"]
+    mt = warmup_state["model_type"]
+    if mt == "cogvideox":
+        t = warmup_state["text_token_num"] // bs
+        return mask[:, t:, t:]
+    if mt == "hunyuan":
+        v = warmup_state["video_token_num"] // bs
+        return mask[:, :v, :v]
+    return mask
+
+
+def SparseAttentionWithMap(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    warmup_state: Dict,
+    logger: logging.Logger,
+    pre_defined_mask: Optional[torch.Tensor] = None,
+    current_step: int = 0,
+    layer_idx: int = 0,
+    use_dense: bool = False,
+    in_test: bool = False,
+    **kwargs,
+):
+    """One attention call of the MOD-DiT schedule; MoD/mod/attn_mask.py:567-729.
+
+    Returns (output (1,H,S,D), mask_info) with the same branch-dependent mask_info as
+    the reference: a dict on dense and sparse steps, the next-step mask (or None) on
+    warmup steps.
+    """
+    if use_dense:
+        output = _dense_engine(query, key, value, pre_defined_mask)
+        return output, {"mode": "warmup", "mask": None}
+    sparse_type = warmup_state["sparse_type"]
+    if sparse_type != "mod-dit":
+        raise NotImplementedError(f"sparse_type {sparse_type!r} is not part of this build")
+
+    num_heads = query.size(1)
+    seq_len = query.size(2)
+    W = warmup_state["warmup_steps"]
+    if current_step < W:
+        if current_step < W - 2:
+            raise RuntimeError(
+                "SparseAttentionWithMap: steps before warmup_steps-2 run dense attention; "
+                "call with use_dense=True (the processors' use_dense gate)"
+            )
+        output, block_sparse_map = flash_attn_with_sparsity_map(
+            query, key, value, threshold=warmup_state["threshold"],
+            block_size=warmup_state["block_size"], model_type=warmup_state["model_type"],
+            video_token_num=warmup_state["video_token_num"],
+            text_token_num=warmup_state["text_token_num"])
+        update_warmup(warmup_state, current_step, block_sparse_map.squeeze(0))
+        if current_step == W - 1:
+            info = predict_mask_from_warmup(warmup_state, seq_len, top_k=warmup_state["top_k"],
+                                            layer_idx=layer_idx)
+            warmup_state["mask"] = info["mask"]
+            warmup_state["_tiles"] = info.get("_tiles")
+            warmup_state["_tiles_for"] = info["mask"]
+            _log_sparsity(logger, layer_idx, warmup_state["mask"])
+            warmup_state["mode"] = info["mode"]
+        return output, warmup_state["mask"]
+
+    if warmup_state.get("mask", None) is None:
+        raise RuntimeError("SparseAttentionWithMap: no mask was predicted during warmup")
+    T = warmup_state["predict_T"]
+    if (current_step - W) % T == T - 1:
+        output, current_sparse_map = flash_attn_with_sparsity_map(
+            query, key, value, threshold=warmup_state["threshold"],
+            block_size=warmup_state["block_size"], model_type=warmup_state["model_type"],
+            video_token_num=warmup_state["video_token_num"],
+            text_token_num=warmup_state["text_token_num"])
+        current_sparse_map = current_sparse_map.squeeze(0)
+        current_mask = _video_part(warmup_state, warmup_state["mask"])
+        warmup_state["prev_full_maps"] = ops.refresh_merge(
+            warmup_state["prev_full_maps"], current_sparse_map, current_mask)
+        features = extract_attention_features(
+            warmup_state=warmup_state, S_T=warmup_state["prev_full_maps"], layer_idx=layer_idx,
+            blocks_per_frame=warmup_state["blocks_per_frame"], use_cuda=warmup_state["use_cuda"])
+        warmup_state["features_history"].append(features)
+        warmup_state["features_history"].pop(0)
+        selected = _select_i32(warmup_state["features_history"], warmup_state["top_k"],
+                               warmup_state.get("predict_T", None))
+        next_mask, tiles = _generate_mask_and_tiles(
+            warmup_state, num_heads, seq_len, warmup_state["blocks_per_frame"], selected,
+            warmup_state["mode"], device=query.device)
+        warmup_state["mask"] = next_mask
+        warmup_state["_tiles"] = tiles
+        warmup_state["_tiles_for"] = next_mask
+    else:
+        mask = warmup_state["mask"]
+        tiles = warmup_state.get("_tiles") if warmup_state.get("_tiles_for") is mask else None
+        output = _engine(query, key, value, mask, tiles, pre_defined_mask,
+                         warmup_state.get("video_token_num", 0), warmup_state["block_size"],
+                         warmup_state.get("tile_rows", "union") == "union")
+    return output, {"mask": warmup_state["mask"]}

@@ -1,0 +1,423 @@
+// Dense and block-sparse flash-attention forward for gfx950 (CDNA4).
+//
+// One workgroup = 4 wave64s = 128 query rows (each wave owns 32 rows); keys stream in
+// tiles of 64 (the mask's key-block granularity). Per key tile each wave computes
+//   S^T (64 keys x 32 queries) = K . Q^T      with 2 x 8 (d=128) bf16 MFMA 32x32x16
+//   O^T (d x 32 queries)      += V^T . P^T    with (d/32) x 4 MFMA 32x32x16
+// Computing the transposed products puts one query per lane column, so the running
+// row max / row sum live in one lane (plus one exchange with the lane 32 apart) and
+// the rescale of O is a per-lane multiply. The S^T accumulator layout is exactly the
+// B-operand layout P^T needs, so P never leaves registers.
+//
+// LDS per stage: K row-major [64][d] (pitch 2d+16 B) and V transposed [d][64]
+// (pitch 136 B); two stages double-buffer the tiles, filled from registers that were
+// loaded from global memory during the previous tile's math.
+//
+// The sparse variant walks a per-(head, query tile) list of key tiles, each entry
+// carrying two row bits (query rows 0-63 / 64-127 of the tile); a wave whose bit is
+// clear skips the math but still helps stage the tile.
+//
+// Reference semantics: flash_attn_func (MoD/mod/triton_flash_sparsity.py:320-321) for
+// the dense pass incl. its LSE; block_sparse_sage2_attn_cuda at 128q x 64k tiles
+// (MoD/mod/attn_mask.py:296-317) for the sparse pass, computed here in bf16/fp16 with
+// fp32 softmax instead of SageAttention's quantisation.
+#include "common.h"
+
+namespace moddit {
+namespace {
+
+constexpr int kBM = 128;  // query rows per workgroup
+constexpr int kBN = 64;   // keys per tile
+constexpr int kThreads = 256;
+
+template <int D>
+struct AttnLds {
+  static constexpr int kPitchK = D * 2 + 16;  // bytes per K row
+  static constexpr int kPitchV = kBN * 2 + 8;  // bytes per V^T row
+  static constexpr int kKBytes = kBN * kPitchK;
+  static constexpr int kVBytes = D * kPitchV;
+  static constexpr int kStage = kKBytes + kVBytes;
+  static constexpr int kTotal = 2 * kStage;
+};
+
+struct AttnParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  float* lse;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int heads;
+  int q_len;
+  int kv_len;
+  int n_qtiles;
+  int n_ktiles;
+  float scale_log2;  // softmax_scale * log2(e)
+  const int32_t* counts;
+  const int32_t* entries;
+  int cap;
+};
+
+template <int D, typename E, bool kSparse>
+__global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p) {
+  using L = AttnLds<D>;
+  using V8 = typename E::vec8;
+  constexpr int kDChunks = D / 16;       // MFMA k-steps over d for S^T
+  constexpr int kDSub = D / 32;          // 32-row blocks of O^T
+  constexpr int kVecPerRow = D / 8;      // 16-byte vectors per token row
+  constexpr int kKVecs = kBN * kVecPerRow / kThreads;  // K vectors per thread
+  constexpr int kKeysPerGroup = D / 32;  // V keys per thread (x 8 dims)
+
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int half = lane >> 5;
+  const int c32 = lane & 31;
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = tile % p.n_qtiles;
+  const int bh = tile / p.n_qtiles;
+  const int b = bh / p.heads;
+  const int h = bh - b * p.heads;
+
+  const uint16_t* qb = p.q + b * p.q_sb + h * p.q_sh;
+  const uint16_t* kb = p.k + b * p.k_sb + h * p.k_sh;
+  const uint16_t* vb = p.v + b * p.v_sb + h * p.v_sh;
+
+  // ---- tile list ----
+  int n_iter;
+  const int32_t* list = nullptr;
+  if (kSparse) {
+    const int64_t slot = static_cast<int64_t>(h) * p.n_qtiles + qt;
+    n_iter = p.counts[slot];
+    n_iter = n_iter < 0 ? 0 : (n_iter < p.cap ? n_iter : p.cap);
+    list = p.entries + slot * p.cap;
+  } else {
+    n_iter = p.n_ktiles;
+  }
+  const int wbit = 1 << (wave >> 1);
+
+  // ---- Q fragments (B operand of S^T = K Q^T): lane holds query c32, dims 8*half.. ----
+  const int q_row = qt * kBM + wave * 32 + c32;
+  V8 qf[kDChunks];
+  {
+    const int r = q_row < p.q_len ? q_row : p.q_len - 1;
+    const u32x4* src = reinterpret_cast<const u32x4*>(qb + r * p.q_ss);
+#pragma unroll
+    for (int c = 0; c < kDChunks; ++c) qf[c] = as_vec8<V8>(src[2 * c + half]);
+  }
+
+  // ---- global -> register staging of one K/V tile ----
+  u32x4 kreg[kKVecs];
+  u32x4 vreg[kKeysPerGroup];
+  const int v_dgrp = tid % (D / 8);
+  const int v_kgrp = tid / (D / 8);
+
+#define MODDIT_LOAD_TILE(KT)                                                        \
+  do {                                                                              \
+    const int key0_ = (KT) * kBN;                                                   \
+    _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_) {                         \
+      const int vec_ = tid + i_ * kThreads;                                         \
+      int key_ = key0_ + vec_ / kVecPerRow;                                         \
+      key_ = key_ < p.kv_len ? key_ : p.kv_len - 1;                                 \
+      kreg[i_] = reinterpret_cast<const u32x4*>(kb + key_ * p.k_ss)[vec_ % kVecPerRow]; \
+    }                                                                               \
+    _Pragma("unroll") for (int j_ = 0; j_ < kKeysPerGroup; ++j_) {                  \
+      int key_ = key0_ + v_kgrp * kKeysPerGroup + j_;                               \
+      key_ = key_ < p.kv_len ? key_ : p.kv_len - 1;                                 \
+      vreg[j_] = reinterpret_cast<const u32x4*>(vb + key_ * p.v_ss)[v_dgrp];        \
+    }                                                                               \
+  } while (0)
+
+#define MODDIT_STORE_TILE(STAGE)                                                    \
+  do {                                                                              \
+    unsigned char* ks_ = smem + (STAGE) * L::kStage;                                \
+    unsigned char* vs_ = ks_ + L::kKBytes;                                          \
+    _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_) {                         \
+      const int vec_ = tid + i_ * kThreads;                                         \
+      *reinterpret_cast<u32x4*>(ks_ + (vec_ / kVecPerRow) * L::kPitchK +            \
+                                (vec_ % kVecPerRow) * 16) = kreg[i_];               \
+    }                                                                               \
+    /* V^T: dim (v_dgrp*8 + dd), keys v_kgrp*kKeysPerGroup + 0.. */                 \
+    _Pragma("unroll") for (int dd_ = 0; dd_ < 8; ++dd_) {                           \
+      unsigned char* dst_ =                                                         \
+          vs_ + (v_dgrp * 8 + dd_) * L::kPitchV + v_kgrp * kKeysPerGroup * 2;       \
+      if constexpr (kKeysPerGroup == 4) {                                           \
+        u32x2 w_;                                                                   \
+        w_.x = pack2(u16_at(vreg[0], dd_), u16_at(vreg[1], dd_));                   \
+        w_.y = pack2(u16_at(vreg[2], dd_), u16_at(vreg[3], dd_));                   \
+        *reinterpret_cast<u32x2*>(dst_) = w_;                                       \
+      } else {                                                                      \
+        *reinterpret_cast<uint32_t*>(dst_) =                                        \
+            pack2(u16_at(vreg[0], dd_), u16_at(vreg[1], dd_));                      \
+      }                                                                             \
+    }                                                                               \
+  } while (0)
+
+  f32x16 oacc[kDSub];
+#pragma unroll
+  for (int i = 0; i < kDSub; ++i) oacc[i] = f32x16{};
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+
+  auto tile_of = [&](int it, int& kt, int& flags) {
+    if (kSparse) {
+      // Entries come from the tile-list builders; clamp anyway so a corrupt list can
+      // only select a wrong (in-bounds) tile, never address outside K/V.
+      const int e = list[it];
+      kt = e >> 2;
+      kt = kt < 0 ? 0 : (kt < p.n_ktiles ? kt : p.n_ktiles - 1);
+      flags = e & 3;
+    } else {
+      kt = it;
+      flags = 3;
+    }
+  };
+
+  if (n_iter > 0) {
+    int kt0, fl0;
+    tile_of(0, kt0, fl0);
+    MODDIT_LOAD_TILE(kt0);
+    MODDIT_STORE_TILE(0);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < n_iter; ++it) {
+    int kt, flags;
+    tile_of(it, kt, flags);
+    const bool has_next = it + 1 < n_iter;
+    if (has_next) {
+      int kn, fn;
+      tile_of(it + 1, kn, fn);
+      MODDIT_LOAD_TILE(kn);
+    }
+
+    if (flags & wbit) {
+      const unsigned char* ks = smem + (it & 1) * L::kStage;
+      const unsigned char* vs = ks + L::kKBytes;
+
+      // S^T = K . Q^T, two 32-key halves.
+      f32x16 s0 = f32x16{};
+      f32x16 s1 = f32x16{};
+#pragma unroll
+      for (int c = 0; c < kDChunks; ++c) {
+        const V8 a0 = *reinterpret_cast<const V8*>(ks + c32 * L::kPitchK + c * 32 + half * 16);
+        const V8 a1 =
+            *reinterpret_cast<const V8*>(ks + (32 + c32) * L::kPitchK + c * 32 + half * 16);
+        s0 = E::mma(a0, qf[c], s0);
+        s1 = E::mma(a1, qf[c], s1);
+      }
+
+      const int key0 = kt * kBN;
+      if (key0 + kBN > p.kv_len) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kr = 8 * (i >> 2) + 4 * half + (i & 3);
+          if (key0 + kr >= p.kv_len) s0[i] = -INFINITY;
+          if (key0 + 32 + kr >= p.kv_len) s1[i] = -INFINITY;
+        }
+      }
+
+      float mx = s0[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s0[i]);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s1[i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+
+      const float m_new = fmaxf(m_run, mx * p.scale_log2);
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+
+      V8 pb[4];
+      float rs = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], p.scale_log2, -m_use));
+        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], p.scale_log2, -m_use));
+        rs += e0 + e1;
+        pb[i >> 3][i & 7] = static_cast<typename E::elem>(e0);
+        pb[2 + (i >> 3)][i & 7] = static_cast<typename E::elem>(e1);
+      }
+      l_run = l_run * alpha + rs;
+      m_run = m_new;
+
+#pragma unroll
+      for (int dsub = 0; dsub < kDSub; ++dsub) {
+        oacc[dsub] *= alpha;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const unsigned char* row = vs + (dsub * 32 + c32) * L::kPitchV + c * 32 + half * 8;
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
+          const u32x4 a = {lo.x, lo.y, hi.x, hi.y};
+          oacc[dsub] = E::mma(as_vec8<V8>(a), pb[c], oacc[dsub]);
+        }
+      }
+    }
+
+    if (has_next) MODDIT_STORE_TILE((it + 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue ----
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (q_row < p.q_len) {
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + q_row * p.o_ss;
+#pragma unroll
+    for (int dsub = 0; dsub < kDSub; ++dsub) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = dsub * 32 + 8 * g + 4 * half;
+        u32x2 w;
+        w.x = pack2(E::from_float(oacc[dsub][4 * g + 0] * inv),
+                    E::from_float(oacc[dsub][4 * g + 1] * inv));
+        w.y = pack2(E::from_float(oacc[dsub][4 * g + 2] * inv),
+                    E::from_float(oacc[dsub][4 * g + 3] * inv));
+        *reinterpret_cast<u32x2*>(orow + d) = w;
+      }
+    }
+    if (p.lse != nullptr && half == 0) {
+      const int64_t li = static_cast<int64_t>(bh) * p.q_len + q_row;
+      p.lse[li] = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+    }
+  }
+}
+
+#undef MODDIT_LOAD_TILE
+#undef MODDIT_STORE_TILE
+
+template <int D, typename E, bool kSparse>
+int launch_attention(const AttnParams& p, int batch, hipStream_t stream) {
+  using L = AttnLds<D>;
+  auto kernel = attention_fwd_kernel<D, E, kSparse>;
+  static bool configured = false;  // the attribute is per function, same on every device
+  if (!configured) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, L::kTotal) != hipSuccess) {
+      set_error("attention: cannot reserve %d bytes of LDS", L::kTotal);
+      return MODDIT_EHIP;
+    }
+    configured = true;
+  }
+  const int64_t tiles = static_cast<int64_t>(batch) * p.heads * p.n_qtiles;
+  if (tiles == 0) return MODDIT_OK;
+  if (tiles > 0x7fffffff) {
+    set_error("attention: too many tiles (%lld)", static_cast<long long>(tiles));
+    return MODDIT_EINVAL;
+  }
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), L::kTotal,
+                     stream, p);
+  MODDIT_CHECK_LAUNCH("attention");
+  return MODDIT_OK;
+}
+
+int attention_entry(const void* q, const void* k, const void* v, void* o, float* lse, int batch,
+                    int heads, int q_len, int kv_len, int head_dim, const int64_t* qs,
+                    const int64_t* ks, const int64_t* vs, const int64_t* os, float scale,
+                    int dtype, const int32_t* counts, const int32_t* entries, int n_qtiles,
+                    int cap, moddit_stream_t stream) {
+  clear_error();
+  MODDIT_CHECK_ARG(q && k && v && o, "attention: null tensor pointer");
+  MODDIT_CHECK_ARG(qs && ks && vs && os, "attention: null stride array");
+  MODDIT_CHECK_ARG(scale > 0.f && std::isfinite(scale), "attention: softmax_scale must be positive");
+  MODDIT_CHECK_ARG(batch >= 0 && heads >= 0 && q_len >= 0 && kv_len >= 0,
+                   "attention: negative size");
+  if (head_dim != 64 && head_dim != 128) {
+    set_error("attention: head_dim must be 64 or 128, got %d", head_dim);
+    return MODDIT_EUNSUPPORTED;
+  }
+  if (dtype != MODDIT_BF16 && dtype != MODDIT_FP16) {
+    set_error("attention: dtype must be bf16 or fp16");
+    return MODDIT_EUNSUPPORTED;
+  }
+  MODDIT_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
+                   "attention: q/k/v/o must be 16-byte aligned");
+  const int64_t* all[4] = {qs, ks, vs, os};
+  for (int t = 0; t < 4; ++t)
+    for (int j = 0; j < 3; ++j)
+      MODDIT_CHECK_ARG(all[t][j] >= 0 && all[t][j] % 8 == 0,
+                       "attention: strides must be non-negative multiples of 8 elements");
+  const bool sparse = counts != nullptr;
+  const int nq = (q_len + kBM - 1) / kBM;
+  if (sparse) {
+    MODDIT_CHECK_ARG(entries != nullptr, "attention: tile entries missing");
+    MODDIT_CHECK_ARG(n_qtiles == nq, "attention: n_qtiles=%d but q_len=%d needs %d", n_qtiles,
+                     q_len, nq);
+    MODDIT_CHECK_ARG(cap > 0, "attention: cap must be positive");
+  }
+  if (q_len == 0 || batch == 0 || heads == 0) return MODDIT_OK;
+  MODDIT_CHECK_ARG(kv_len > 0 || sparse, "attention: kv_len must be positive for dense attention");
+
+  AttnParams p;
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.o = static_cast<uint16_t*>(o);
+  p.lse = lse;
+  p.q_sb = qs[0]; p.q_sh = qs[1]; p.q_ss = qs[2];
+  p.k_sb = ks[0]; p.k_sh = ks[1]; p.k_ss = ks[2];
+  p.v_sb = vs[0]; p.v_sh = vs[1]; p.v_ss = vs[2];
+  p.o_sb = os[0]; p.o_sh = os[1]; p.o_ss = os[2];
+  p.heads = heads;
+  p.q_len = q_len;
+  p.kv_len = kv_len;
+  p.n_qtiles = nq;
+  p.n_ktiles = (kv_len + kBN - 1) / kBN;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.counts = counts;
+  p.entries = entries;
+  p.cap = cap;
+  if (sparse && kv_len == 0) {
+    set_error("attention: kv_len must be positive");
+    return MODDIT_EINVAL;
+  }
+
+  hipStream_t st = as_stream(stream);
+  const bool bf = dtype == MODDIT_BF16;
+  if (head_dim == 128) {
+    if (bf) return sparse ? launch_attention<128, Bf16, true>(p, batch, st)
+                          : launch_attention<128, Bf16, false>(p, batch, st);
+    return sparse ? launch_attention<128, Fp16, true>(p, batch, st)
+                  : launch_attention<128, Fp16, false>(p, batch, st);
+  }
+  if (bf) return sparse ? launch_attention<64, Bf16, true>(p, batch, st)
+                        : launch_attention<64, Bf16, false>(p, batch, st);
+  return sparse ? launch_attention<64, Fp16, true>(p, batch, st)
+                : launch_attention<64, Fp16, false>(p, batch, st);
+}
+
+}  // namespace
+}  // namespace moddit
+
+extern "C" int moddit_flash_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                                int batch, int heads, int q_len, int kv_len, int head_dim,
+                                const int64_t q_strides[3], const int64_t k_strides[3],
+                                const int64_t v_strides[3], const int64_t o_strides[3],
+                                float softmax_scale, int dtype, moddit_stream_t stream) {
+  return moddit::attention_entry(q, k, v, o, lse, batch, heads, q_len, kv_len, head_dim,
+                                 q_strides, k_strides, v_strides, o_strides, softmax_scale, dtype,
+                                 nullptr, nullptr, 0, 0, stream);
+}
+
+extern "C" int moddit_block_sparse_fwd(const void* q, const void* k, const void* v, void* o,
+                                       float* lse, int batch, int heads, int q_len, int kv_len,
+                                       int head_dim, const int64_t q_strides[3],
+                                       const int64_t k_strides[3], const int64_t v_strides[3],
+                                       const int64_t o_strides[3], float softmax_scale, int dtype,
+                                       const int32_t* counts, const int32_t* entries,
+                                       int n_qtiles, int cap, moddit_stream_t stream) {
+  if (counts == nullptr) {
+    moddit::set_error("block_sparse_fwd: counts must not be NULL");
+    return MODDIT_EINVAL;
+  }
+  return moddit::attention_entry(q, k, v, o, lse, batch, heads, q_len, kv_len, head_dim,
+                                 q_strides, k_strides, v_strides, o_strides, softmax_scale, dtype,
+                                 counts, entries, n_qtiles, cap, stream);
+}

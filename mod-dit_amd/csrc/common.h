@@ -1,0 +1,121 @@
+// Shared device/host helpers for the gfx950 kernels of the MOD-DiT hot path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/moddit.h"
+
+namespace moddit {
+
+// ---------------------------------------------------------------------------------
+// Error reporting: a thread-local message behind integer status codes.
+// ---------------------------------------------------------------------------------
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+#define MODDIT_CHECK_ARG(cond, ...)          \
+  do {                                       \
+    if (!(cond)) {                           \
+      ::moddit::set_error(__VA_ARGS__);      \
+      return MODDIT_EINVAL;                  \
+    }                                        \
+  } while (0)
+
+#define MODDIT_CHECK_LAUNCH(what)                                                   \
+  do {                                                                              \
+    hipError_t err_ = hipGetLastError();                                            \
+    if (err_ != hipSuccess) {                                                       \
+      ::moddit::set_error("%s: launch failed: %s", what, hipGetErrorString(err_)); \
+      return MODDIT_EHIP;                                                           \
+    }                                                                               \
+  } while (0)
+
+inline hipStream_t as_stream(moddit_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------------
+// Vector types for MFMA operands and 16-byte moves.
+// ---------------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef _Float16 f16x8 __attribute__((__vector_size__(8 * sizeof(_Float16))));
+typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
+// Native vectors for raw 16/8-byte moves (HIP's uint4 struct defeats register promotion).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Storage element traits: both 16-bit types are moved as raw uint16_t.
+struct Bf16 {
+  typedef bf16x8 vec8;
+  typedef __bf16 elem;
+  static __device__ __forceinline__ f32x16 mma(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float to_float(uint16_t u) {
+    return __uint_as_float(static_cast<uint32_t>(u) << 16);
+  }
+  // Round-to-nearest-even; NaN stays a quiet NaN.
+  static __device__ __forceinline__ uint16_t from_float(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+  }
+};
+
+struct Fp16 {
+  typedef f16x8 vec8;
+  typedef _Float16 elem;
+  static __device__ __forceinline__ f32x16 mma(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float to_float(uint16_t u) {
+    _Float16 h;
+    __builtin_memcpy(&h, &u, 2);
+    return static_cast<float>(h);
+  }
+  static __device__ __forceinline__ uint16_t from_float(float f) {
+    _Float16 h = static_cast<_Float16>(f);  // round-to-nearest-even
+    uint16_t u;
+    __builtin_memcpy(&u, &h, 2);
+    return u;
+  }
+};
+
+template <typename V>
+__device__ __forceinline__ V as_vec8(u32x4 x) {
+  return __builtin_bit_cast(V, x);
+}
+
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+}
+
+__device__ __forceinline__ uint16_t u16_at(const u32x4& v, int i) {
+  const uint32_t w = v[i >> 1];
+  return static_cast<uint16_t>((i & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+// ---------------------------------------------------------------------------------
+// Workgroup -> tile mapping that keeps consecutive tiles on one XCD.
+// The dispatcher hands workgroup w to XCD (w % 8); remapping makes XCD x own one
+// contiguous range of logical tiles so tiles that share K/V share that XCD's L2.
+// ---------------------------------------------------------------------------------
+constexpr int kNumXcd = 8;
+
+__device__ __forceinline__ int xcd_remap(int wg, int total) {
+  const int xcd = wg % kNumXcd;
+  const int local = wg / kNumXcd;
+  const int base = total / kNumXcd;
+  const int rem = total % kNumXcd;
+  return xcd * base + (xcd < rem ? xcd : rem) + local;
+}
+
+}  // namespace moddit

@@ -1,0 +1,297 @@
+"""Torch-facing wrappers over the C ABI (include/moddit.h).
+
+Tensors are only plumbing here: each function validates shapes, allocates outputs with
+torch on the input's device, and launches the HIP kernel on torch's current stream.
+Nothing in this module computes on the host, and nothing falls back to torch math.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import check, strides3
+
+_DTYPES = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16}
+
+
+def _stream(t: torch.Tensor):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _require_gpu(*tensors: torch.Tensor, what: str) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError(f"{what}: tensors must live on a GPU (got {t.device})")
+
+
+def _attn_view(t: torch.Tensor) -> torch.Tensor:
+    """(B,H,S,D) with unit dim stride, 16-byte aligned; copies only if needed."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:3]):
+        t = t.contiguous()
+    return t
+
+
+def _attn_dtype(t: torch.Tensor) -> int:
+    if t.dtype not in _DTYPES:
+        raise TypeError(f"expected float16 or bfloat16 inputs, got {t.dtype}")
+    return _DTYPES[t.dtype]
+
+
+# --------------------------------------------------------------------------------------
+# attention
+# --------------------------------------------------------------------------------------
+@dataclass
+class TileList:
+    """Per-(head, 128-row query tile) ascending lists of active 64-key tiles.
+
+    entries[h, t, i] = (key_tile << 2) | row_bits for i < counts[h, t]; bit 0 enables the
+    tile for query rows 0..63 of the query tile, bit 1 for rows 64..127.
+    """
+
+    counts: torch.Tensor   # (H, n_qtiles) int32
+    entries: torch.Tensor  # (H, n_qtiles, cap) int32
+    block_size: int
+    union_rows: bool
+
+    @property
+    def n_qtiles(self) -> int:
+        return self.counts.shape[1]
+
+    @property
+    def cap(self) -> int:
+        return self.entries.shape[2]
+
+    def active_tile_pairs(self) -> torch.Tensor:
+        """Executed (64-row query block, 64-key tile) pairs per head (device tensor)."""
+        bits = (self.entries & 1) + ((self.entries >> 1) & 1)
+        idx = torch.arange(self.cap, device=self.entries.device).view(1, 1, -1)
+        valid = idx < self.counts.unsqueeze(-1)
+        return (bits * valid).sum(dim=(1, 2))
+
+
+def _attention(q, k, v, scale, return_lse, tiles: TileList | None, out=None):
+    _require_gpu(q, k, v, what="attention")
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("query, key and value must have shape [B, H, S, D]")
+    if k.shape != v.shape or q.shape[:2] != k.shape[:2] or q.shape[3] != k.shape[3]:
+        raise ValueError(f"incompatible shapes q={tuple(q.shape)} k={tuple(k.shape)} v={tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("query, key, and value must have the same dtype")
+    dt = _attn_dtype(q)
+    B, H, Sq, D = q.shape
+    Skv = k.shape[2]
+    if D not in (64, 128):
+        raise ValueError(f"head_dim must be 64 or 128, got {D}")
+    q, k, v = _attn_view(q), _attn_view(k), _attn_view(v)
+    if out is None:
+        out = torch.empty((B, H, Sq, D), device=q.device, dtype=q.dtype)
+    lse = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32) if return_lse else None
+    if scale is None:
+        scale = D ** -0.5
+    lib = _lib.load()
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), _ptr(lse), B, H, Sq, Skv, D,
+            strides3(*q.stride()[:3]), strides3(*k.stride()[:3]), strides3(*v.stride()[:3]),
+            strides3(*out.stride()[:3]), float(scale), dt)
+    if tiles is None:
+        check(lib.moddit_flash_fwd(*args, _stream(q)), "moddit_flash_fwd")
+    else:
+        if tiles.counts.shape[0] != H:
+            raise ValueError(f"tile lists cover {tiles.counts.shape[0]} heads, attention has {H}")
+        check(lib.moddit_block_sparse_fwd(*args, tiles.counts.data_ptr(), tiles.entries.data_ptr(),
+                                          tiles.n_qtiles, tiles.cap, _stream(q)),
+              "moddit_block_sparse_fwd")
+    return out, lse
+
+
+def flash_fwd(q, k, v, softmax_scale=None, return_lse=True, out=None):
+    """Dense attention over all keys; returns (O (B,H,Sq,D), LSE (B,H,Sq) fp32 or None)."""
+    return _attention(q, k, v, softmax_scale, return_lse, None, out)
+
+
+def block_sparse_fwd(q, k, v, tiles: TileList, softmax_scale=None, return_lse=False, out=None):
+    """Attention restricted to the active key tiles of `tiles`."""
+    return _attention(q, k, v, softmax_scale, return_lse, tiles, out)
+
+
+# --------------------------------------------------------------------------------------
+# sparsity map replay
+# --------------------------------------------------------------------------------------
+def sparsity_map(query, key, lse, *, softmax_scale, log_threshold, q_video_offset,
+                 k_video_offset, video_blocks, block_size):
+    """fp16 (B,H,n,n) map of MoD/mod/cuda_flash_sparsity.py:71-99 on the HIP replay kernel."""
+    _require_gpu(query, key, lse, what="sparsity_map")
+    if query.ndim != 4 or key.ndim != 4 or query.shape != key.shape:
+        raise RuntimeError("Q and K must have identical shape [B, H, S, D]")
+    if lse.ndim != 3 or tuple(lse.shape) != tuple(query.shape[:3]):
+        raise RuntimeError("LSE shape must match Q except for head_dim")
+    if lse.dtype != torch.float32:
+        raise RuntimeError("LSE must be float32")
+    if query.dtype != key.dtype:
+        raise RuntimeError("Q and K dtypes must match")
+    dt = _attn_dtype(query)
+    B, H, S, D = query.shape
+    query, key = _attn_view(query), _attn_view(key)
+    lse = lse.contiguous()
+    out = torch.empty((B, H, video_blocks, video_blocks), device=query.device, dtype=torch.float16)
+    lib = _lib.load()
+    check(lib.moddit_sparsity_map(query.data_ptr(), key.data_ptr(), lse.data_ptr(), out.data_ptr(),
+                                  B, H, S, D, strides3(*query.stride()[:3]),
+                                  strides3(*key.stride()[:3]), float(softmax_scale),
+                                  float(log_threshold), int(q_video_offset), int(k_video_offset),
+                                  int(video_blocks), int(block_size), dt, _stream(query)),
+          "moddit_sparsity_map")
+    return out
+
+
+# --------------------------------------------------------------------------------------
+# least squares
+# --------------------------------------------------------------------------------------
+def compute_mts(S_T: torch.Tensor, blocks_per_frame: int) -> torch.Tensor:
+    """(H, 3n) fp32 M^T S of an (H,n,n) fp16 or fp32 map."""
+    _require_gpu(S_T, what="compute_mts")
+    if S_T.ndim != 3 or S_T.shape[1] != S_T.shape[2]:
+        raise ValueError(f"S_T must have shape (H, n, n), got {tuple(S_T.shape)}")
+    if S_T.dtype == torch.float16:
+        dt = _lib.FP16
+    elif S_T.dtype == torch.float32:
+        dt = _lib.FP32
+    else:
+        raise TypeError(f"S_T must be float16 or float32, got {S_T.dtype}")
+    S_T = S_T.contiguous()
+    H, n, _ = S_T.shape
+    out = torch.empty((H, 3 * n), device=S_T.device, dtype=torch.float32)
+    check(_lib.load().moddit_mts(S_T.data_ptr(), dt, H, n, int(blocks_per_frame), out.data_ptr(),
+                                 _stream(S_T)), "moddit_mts")
+    return out
+
+
+def compute_mtm_host(n: int, blocks_per_frame: int, regularization: float) -> torch.Tensor:
+    """Closed-form M^T M + lambda I as a CPU float64 (3n, 3n) tensor."""
+    F = 3 * n
+    out = torch.empty((F, F), dtype=torch.float64)
+    check(_lib.load().moddit_mtm_host(int(n), int(blocks_per_frame), float(regularization),
+                                      out.data_ptr()), "moddit_mtm_host")
+    return out
+
+
+def solve(ginv: torch.Tensor, mts: torch.Tensor) -> torch.Tensor:
+    """X = Ginv . MTS^T per head: (H, F) fp32."""
+    _require_gpu(ginv, mts, what="solve")
+    H, F = mts.shape
+    if ginv.shape != (F, F) or ginv.dtype != torch.float32 or mts.dtype != torch.float32:
+        raise ValueError("solve expects ginv (F,F) fp32 and mts (H,F) fp32")
+    ginv, mts = ginv.contiguous(), mts.contiguous()
+    x = torch.empty_like(mts)
+    check(_lib.load().moddit_solve(ginv.data_ptr(), mts.data_ptr(), x.data_ptr(), H, F,
+                                   _stream(mts)), "moddit_solve")
+    return x
+
+
+# --------------------------------------------------------------------------------------
+# line selection / modes / mask
+# --------------------------------------------------------------------------------------
+def select_lines(x_cur: torch.Tensor, x_last: torch.Tensor, n: int, predict_T: int,
+                 top_k: int) -> torch.Tensor:
+    """(H, k) int32 ascending indices of the k smallest predicted line scores."""
+    _require_gpu(x_cur, x_last, what="select_lines")
+    H, F = x_cur.shape
+    if F != 3 * n or x_last.shape != x_cur.shape:
+        raise ValueError("x_cur/x_last must be (H, 3n)")
+    if predict_T is None:
+        raise TypeError("predict_T must be an int")
+    k = min(int(top_k), 3 * n - 1)
+    sel = torch.empty((H, k), device=x_cur.device, dtype=torch.int32)
+    check(_lib.load().moddit_select_lines(x_cur.contiguous().data_ptr(),
+                                          x_last.contiguous().data_ptr(), H, n, int(predict_T),
+                                          int(top_k), sel.data_ptr(), _stream(x_cur)),
+          "moddit_select_lines")
+    return sel
+
+
+def check_bd(x: torch.Tensor, mode: torch.Tensor, threshold: float) -> torch.Tensor:
+    """In place: mode[h] SPARSE -> BLOCK_DIAGONAL when x[h,-1] <= threshold."""
+    _require_gpu(x, mode, what="check_bd")
+    H, F = x.shape
+    if mode.dtype != torch.uint8 or mode.shape != (H,) or not mode.is_contiguous():
+        raise ValueError("mode must be a contiguous (H,) uint8 tensor")
+    check(_lib.load().moddit_check_bd(x.contiguous().data_ptr(), H, F, float(threshold),
+                                      mode.data_ptr(), _stream(x)), "moddit_check_bd")
+    return mode
+
+
+def _tile_shape(nb: int, block_size: int):
+    tokens = nb * block_size
+    return (tokens + 127) // 128, nb * (block_size // 64)
+
+
+def mask_from_lines(sel, mode, *, n, blocks_per_frame, layout, nb, text_blocks, block_size,
+                    union_rows=True, want_mask=True, want_tiles=True):
+    """Bool mask (H,nb,nb) and/or TileList from selected lines (one fused kernel)."""
+    _require_gpu(sel, mode, what="mask_from_lines")
+    H = mode.shape[0]
+    sel = sel.to(torch.int32).contiguous()
+    if sel.ndim != 2 or sel.shape[0] != H:
+        raise ValueError("selected lines must be (H, k)")
+    dev = sel.device
+    mask = torch.empty((H, nb, nb), device=dev, dtype=torch.bool) if want_mask else None
+    tiles = None
+    nq, cap = _tile_shape(nb, block_size)
+    if want_tiles:
+        tiles = TileList(torch.empty((H, nq), device=dev, dtype=torch.int32),
+                         torch.empty((H, nq, cap), device=dev, dtype=torch.int32),
+                         block_size, bool(union_rows))
+    check(_lib.load().moddit_mask_from_lines(
+        sel.data_ptr(), H, sel.shape[1], mode.data_ptr(), int(n), int(blocks_per_frame),
+        int(layout), int(nb), int(text_blocks), int(block_size), int(bool(union_rows)),
+        _ptr(mask), _ptr(tiles.counts) if tiles else None, _ptr(tiles.entries) if tiles else None,
+        nq, cap, _stream(sel)), "moddit_mask_from_lines")
+    return mask, tiles
+
+
+def mask_to_tiles(mask: torch.Tensor, block_size: int, union_rows=True, kv_tiles=None) -> TileList:
+    """TileList of an explicit bool (H,nb,nb) block mask."""
+    _require_gpu(mask, what="mask_to_tiles")
+    if mask.ndim != 3 or mask.shape[1] != mask.shape[2]:
+        raise ValueError(f"mask must be (H, nb, nb), got {tuple(mask.shape)}")
+    if mask.dtype != torch.bool:
+        mask = mask != 0
+    mask = mask.contiguous()
+    H, nb, _ = mask.shape
+    nq, cap = _tile_shape(nb, block_size)
+    if kv_tiles is None:
+        kv_tiles = cap
+    tiles = TileList(torch.empty((H, nq), device=mask.device, dtype=torch.int32),
+                     torch.empty((H, nq, cap), device=mask.device, dtype=torch.int32),
+                     block_size, bool(union_rows))
+    check(_lib.load().moddit_mask_to_tiles(mask.data_ptr(), H, nb, int(block_size),
+                                           int(bool(union_rows)), int(kv_tiles),
+                                           tiles.counts.data_ptr(), tiles.entries.data_ptr(), nq,
+                                           cap, _stream(mask)), "moddit_mask_to_tiles")
+    return tiles
+
+
+def refresh_merge(prev: torch.Tensor, cur: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    """where(mask, cur, prev) over (H,n,n) fp16 maps; mask may be a strided bool view."""
+    _require_gpu(prev, cur, mask, what="refresh_merge")
+    if prev.shape != cur.shape or prev.ndim != 3 or tuple(mask.shape) != tuple(prev.shape):
+        raise ValueError("refresh_merge: prev/cur/mask must share shape (H, n, n)")
+    if prev.dtype != torch.float16 or cur.dtype != torch.float16:
+        raise TypeError("refresh_merge: maps must be float16")
+    if mask.dtype != torch.bool:
+        raise TypeError("refresh_merge: mask must be bool")
+    if mask.stride(2) != 1:
+        mask = mask.contiguous()
+    prev, cur = prev.contiguous(), cur.contiguous()
+    H, n, _ = prev.shape
+    out = torch.empty_like(prev)
+    check(_lib.load().moddit_refresh_merge(prev.data_ptr(), cur.data_ptr(), mask.data_ptr(),
+                                           mask.stride(0), mask.stride(1), H, n, out.data_ptr(),
+                                           _stream(prev)), "moddit_refresh_merge")
+    return out

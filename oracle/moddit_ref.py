@@ -1,0 +1,479 @@
+"""numpy restatement of the MOD-DiT hot path (test infrastructure only).
+
+Conventions: maps are (H, n, n); features X are (H, 3n) in the column order of M:
+[2n-1 diagonals, offset k-(n-1) = col-row][n columns][1 frame-block-diagonal].
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+__all__ = [
+    "bf16_round", "fp16_round", "build_M", "mtm_closed_form", "mts_loop", "mts_exact",
+    "ridge_solve", "features_from_x", "reconstruct_map", "predict_lines",
+    "choose_topk_lines", "generate_mask_from_lines", "mask_cell", "tiles_from_mask",
+    "token_mask_from_tiles", "token_mask_from_blocks", "masked_attention",
+    "probability_map", "replay_map", "refresh_merge", "step_phase", "video_layout",
+    "MODE_SPARSE", "MODE_BLOCK_DIAGONAL", "MODE_FULL",
+]
+
+MODE_SPARSE, MODE_BLOCK_DIAGONAL, MODE_FULL = 0, 1, 2
+
+
+# --------------------------------------------------------------------------------------
+# rounding helpers
+# --------------------------------------------------------------------------------------
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """Round fp32 values to bfloat16 (round-to-nearest-even), returned as fp32."""
+    x = np.asarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    nan = np.isnan(x)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    out = u.astype(np.uint32).view(np.float32)
+    return np.where(nan, np.float32(np.nan), out).astype(np.float32)
+
+
+def fp16_round(x: np.ndarray) -> np.ndarray:
+    """Round to IEEE half (numpy's cast is round-to-nearest-even), returned as fp32."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+# --------------------------------------------------------------------------------------
+# layouts (MoD/mod/triton_flash_sparsity.py:101-120)
+# --------------------------------------------------------------------------------------
+def video_layout(model_type: str, S: int, video_tokens: int, text_tokens: int, bs: int):
+    """(video_blocks, q_offset, k_offset)."""
+    if model_type == "wan":
+        return S // bs, 0, 0
+    if model_type == "hunyuan":
+        return video_tokens // bs, 0, 0
+    if model_type == "cogvideox":
+        return video_tokens // bs, text_tokens, text_tokens
+    raise ValueError(f"Unknown model_type: {model_type}")
+
+
+# --------------------------------------------------------------------------------------
+# line model (MoD/mod/cuda_lstsq.py)
+# --------------------------------------------------------------------------------------
+def build_M(n: int, bpf: int) -> np.ndarray:
+    """Explicit (n*n, 3n) indicator matrix of the line model (brute force, small n).
+
+    Column k < 2n-1: cells with col-row = k-(n-1); column 2n-1+j: cells of column j;
+    last column: cells inside the n//bpf frame-diagonal bpf x bpf blocks
+    (MoD/mod/cuda_lstsq.py:52-86, cuda_lstsq_kernel.cu:17-162).
+    """
+    nd = 2 * n - 1
+    F = 3 * n
+    M = np.zeros((n * n, F), dtype=np.float64)
+    for r in range(n):
+        for c in range(n):
+            cell = r * n + c
+            M[cell, (c - r) + (n - 1)] = 1.0
+            M[cell, nd + c] = 1.0
+    nb = n // bpf
+    for f in range(nb):
+        for i in range(bpf):
+            for j in range(bpf):
+                M[(f * bpf + i) * n + (f * bpf + j), F - 1] = 1.0
+    return M
+
+
+def mtm_closed_form(n: int, bpf: int, lam: float) -> np.ndarray:
+    """M^T M + lam I from the closed forms of MoD/mod/cuda_lstsq.py:42-89."""
+    nd = 2 * n - 1
+    F = 3 * n
+    G = np.zeros((F, F), dtype=np.float64)
+    offs = np.arange(-(n - 1), n)
+    G[np.arange(nd), np.arange(nd)] = n - np.abs(offs)
+    G[nd + np.arange(n), nd + np.arange(n)] = n
+    cols = np.arange(n)[None, :]
+    o = offs[:, None]
+    dv = np.where(o >= 0, cols >= o, cols < n + o).astype(np.float64)
+    G[:nd, nd:nd + n] = dv
+    G[nd:nd + n, :nd] = dv.T
+    nbk = n // bpf
+    db = np.where(np.abs(offs) < bpf, nbk * (bpf - np.abs(offs)), 0).astype(np.float64)
+    G[:nd, -1] = db
+    G[-1, :nd] = db
+    vb = np.where(np.arange(n) < nbk * bpf, bpf, 0).astype(np.float64)
+    G[nd:nd + n, -1] = vb
+    G[-1, nd:nd + n] = vb
+    G[-1, -1] = nbk * bpf * bpf
+    G += lam * np.eye(F)
+    return G
+
+
+def mts_loop(S: np.ndarray, bpf: int) -> np.ndarray:
+    """M^T S as the reference's CPU fallback loops it, in fp32 (MoD/mod/cuda_lstsq.py:91-139).
+
+    Small n only (pure-Python loop). Sums accumulate in fp32 in the reference's order.
+    """
+    S = np.asarray(S, dtype=np.float32)
+    H, n, _ = S.shape
+    nd = 2 * n - 1
+    out = np.zeros((H, 3 * n), dtype=np.float32)
+    for k in range(nd):
+        off = k - (n - 1)
+        tot = np.zeros(H, dtype=np.float32)
+        if off >= 0:
+            for i in range(n - off):
+                tot = (tot + S[:, i, i + off]).astype(np.float32)
+        else:
+            for i in range(n + off):
+                tot = (tot + S[:, i - off, i]).astype(np.float32)
+        out[:, k] = tot
+    for k in range(n):
+        out[:, nd + k] = S[:, :, k].sum(axis=1, dtype=np.float32)
+    nbk = n // bpf
+    tot = np.zeros(H, dtype=np.float32)
+    for f in range(nbk):
+        s = f * bpf
+        tot = (tot + S[:, s:s + bpf, s:s + bpf].sum(axis=(1, 2), dtype=np.float32)).astype(np.float32)
+    out[:, 3 * n - 1] = tot
+    return out
+
+
+def mts_exact(S16: np.ndarray, bpf: int) -> np.ndarray:
+    """M^T S of an fp16 map: exact sums, each rounded once to fp32.
+
+    Every fp16 value is an integer multiple of 2^-24, so the sums are formed exactly in
+    int64 units of 2^-24 and converted with one round-to-nearest. Equal to mts_loop
+    wherever the fp32 loop is exact (diagonal and column sums of maps whose entries
+    are multiples of 2^-12 with n * 2^12 < 2^24).
+    """
+    S16 = np.asarray(S16, dtype=np.float16)
+    H, n, _ = S16.shape
+    units = np.rint(S16.astype(np.float64) * 2.0 ** 24).astype(np.int64)
+    nd = 2 * n - 1
+    out = np.zeros((H, 3 * n), dtype=np.float32)
+    r = np.arange(n)[:, None]
+    c = np.arange(n)[None, :]
+    dk = (c - r) + (n - 1)
+    for h in range(H):
+        dsum = np.zeros(nd, dtype=np.int64)
+        np.add.at(dsum, dk.ravel(), units[h].ravel())
+        csum = units[h].sum(axis=0)
+        nbk = n // bpf
+        bsum = np.int64(0)
+        for f in range(nbk):
+            s = f * bpf
+            bsum += units[h, s:s + bpf, s:s + bpf].sum()
+        vals = np.concatenate([dsum, csum, [bsum]]).astype(np.int64)
+        out[h] = vals.astype(np.float32) * np.float32(2.0 ** -24)
+    return out
+
+
+def ridge_solve(S: np.ndarray, bpf: int, lam: float) -> np.ndarray:
+    """X = (M^T M + lam I)^-1 M^T S in fp64 (the target of MoD/mod/cuda_lstsq.py:211-264)."""
+    S = np.asarray(S, dtype=np.float64)
+    H, n, _ = S.shape
+    G = mtm_closed_form(n, bpf, lam)
+    mts = np.stack([_mts_f64(S[h], bpf) for h in range(H)])
+    return np.linalg.solve(G, mts.T).T
+
+
+def _mts_f64(S2: np.ndarray, bpf: int) -> np.ndarray:
+    n = S2.shape[0]
+    nd = 2 * n - 1
+    r = np.arange(n)[:, None]
+    c = np.arange(n)[None, :]
+    dk = ((c - r) + (n - 1)).ravel()
+    d = np.zeros(nd)
+    np.add.at(d, dk, S2.ravel())
+    cs = S2.sum(axis=0)
+    nbk = n // bpf
+    b = sum(S2[f * bpf:(f + 1) * bpf, f * bpf:(f + 1) * bpf].sum() for f in range(nbk))
+    return np.concatenate([d, cs, [b]])
+
+
+def features_from_x(X: np.ndarray, n: int) -> Dict[str, np.ndarray]:
+    """Feature slicing of MoD/mod/cuda_lstsq.py:249-261 (c = columns / 2)."""
+    nd = 2 * n - 1
+    X = np.asarray(X, dtype=np.float32)
+    return {"d": X[:, :nd], "c": X[:, nd:nd + n] / np.float32(2), "b_d": X[:, -1]}
+
+
+def reconstruct_map(X: np.ndarray, n: int, bpf: int) -> np.ndarray:
+    """M X per head (MoD/mod/cuda_lstsq.py:271-357, with c given back as 2c)."""
+    X = np.asarray(X, dtype=np.float64)
+    H = X.shape[0]
+    nd = 2 * n - 1
+    out = np.zeros((H, n, n))
+    r = np.arange(n)[:, None]
+    c = np.arange(n)[None, :]
+    for h in range(H):
+        out[h] = X[h, (c - r) + (n - 1)] + X[h, nd + c]
+        for f in range(n // bpf):
+            out[h, f * bpf:(f + 1) * bpf, f * bpf:(f + 1) * bpf] += X[h, -1]
+    return out
+
+
+# --------------------------------------------------------------------------------------
+# line selection (MoD/mod/attn_mask.py:336-370)
+# --------------------------------------------------------------------------------------
+def predict_lines(x_cur: np.ndarray, x_last: np.ndarray, n: int, T: int) -> np.ndarray:
+    """v = cat(pred_c, pred_d), pred = cur + (cur - last) / T, all in fp32 (:358-362)."""
+    nd = 2 * n - 1
+    xc = np.asarray(x_cur, dtype=np.float32)
+    xl = np.asarray(x_last, dtype=np.float32)
+    c_cur = xc[:, nd:nd + n] / np.float32(2)
+    c_last = xl[:, nd:nd + n] / np.float32(2)
+    d_cur = xc[:, :nd]
+    d_last = xl[:, :nd]
+    Tf = np.float32(T)
+    pc = c_cur + (c_cur - c_last) / Tf
+    pd = d_cur + (d_cur - d_last) / Tf
+    return np.concatenate([pc, pd], axis=1).astype(np.float32)
+
+
+def choose_topk_lines(x_cur, x_last, n: int, T: int, top_k: int) -> np.ndarray:
+    """Indices of the k = min(top_k, 3n-1) smallest predictions per head, ascending.
+
+    topk(largest=False, sorted=False) (:363-369) with ties broken by lower index and NaN
+    ordered last; -0.0 and +0.0 compare equal.
+    """
+    v = predict_lines(x_cur, x_last, n, T)
+    k = min(int(top_k), v.shape[1])
+    out = []
+    for h in range(v.shape[0]):
+        row = v[h].astype(np.float64)
+        row = np.where(row == 0.0, 0.0, row)
+        key_nan = np.isnan(row)
+        order = np.lexsort((np.arange(row.size), np.where(key_nan, np.inf, row), key_nan))
+        out.append(np.sort(order[:k]))
+    return np.stack(out).astype(np.int64) if out else np.zeros((0, k), np.int64)
+
+
+# --------------------------------------------------------------------------------------
+# mask generation (MoD/mod/attn_mask.py:440-559)
+# --------------------------------------------------------------------------------------
+def generate_mask_from_lines(sel: np.ndarray, modes: Sequence[int], *, seq_len: int,
+                             block_size: int, video_tokens: int, text_tokens: int,
+                             bpf: int, model_type: str) -> np.ndarray:
+    """Line-by-line restatement of generate_mask_from_lines (bool (H, nb, nb))."""
+    H = len(modes)
+    block_num = seq_len // block_size
+    tb = text_tokens // block_size
+    vb = video_tokens // block_size
+    mask = np.ones((H, block_num, block_num), dtype=bool)
+    video = np.zeros((H, vb, vb), dtype=bool)
+    sel = np.asarray(sel, dtype=np.int64)
+    if sel.ndim == 1:
+        sel = sel[:, None]
+    full = np.array([m == MODE_FULL for m in modes])
+    bd = np.array([m == MODE_BLOCK_DIAGONAL for m in modes])
+    video[full] = True
+    if vb > 0:
+        row = np.arange(vb).reshape(1, vb, 1)
+        col = np.arange(vb).reshape(1, 1, vb)
+        diff = col - row
+        for t in range(sel.shape[1]):
+            idx = sel[:, t]
+            active = ~full
+            if not active.any():
+                break
+            col_case = (idx < vb) & active
+            if col_case.any():
+                eq = (np.arange(vb).reshape(1, vb) == idx.reshape(H, 1)) & col_case.reshape(H, 1)
+                video |= np.broadcast_to(eq[:, None, :], (H, vb, vb))
+            diag_case = (idx >= vb) & active
+            if diag_case.any():
+                offs = idx - (vb - 1) - vb
+                video |= (diff == offs.reshape(H, 1, 1)) & diag_case.reshape(H, 1, 1)
+        if bd.any():
+            rb = (np.arange(vb) // bpf).reshape(vb, 1)
+            cb = (np.arange(vb) // bpf).reshape(1, vb)
+            video |= bd.reshape(H, 1, 1) & (rb == cb)[None]
+    if model_type == "cogvideox":
+        if tb > 0:
+            mask[:, :tb, :] = True
+            mask[:, :, :tb] = True
+        mask[:, tb:, tb:] = video
+    elif model_type == "hunyuan":
+        mask[:, vb:, :] = True
+        mask[:, :, vb:] = True
+        mask[:, :vb, :vb] = video
+    elif model_type == "wan":
+        mask = video
+    else:
+        mask = np.ones_like(mask)
+    return mask
+
+
+def mask_cell(sel_h: Sequence[int], mode: int, n: int, bpf: int, i: int, j: int) -> bool:
+    """Independent per-cell definition of the video mask (used to cross-check)."""
+    if mode == MODE_FULL:
+        return True
+    for idx in sel_h:
+        if 0 <= idx < n and idx == j:
+            return True
+        if n <= idx < 3 * n - 1 and (j - i) == idx - n - (n - 1):
+            return True
+    return mode == MODE_BLOCK_DIAGONAL and i // bpf == j // bpf
+
+
+# --------------------------------------------------------------------------------------
+# attention engine tiles (MoD/mod/attn_mask.py:296-311)
+# --------------------------------------------------------------------------------------
+def tiles_from_mask(mask: np.ndarray, block_size: int, union_rows: bool,
+                    kv_tiles: Optional[int] = None) -> Tuple[np.ndarray, List[List[List[int]]]]:
+    """Per (head, 128-row query tile) ascending entries (key_tile << 2 | row bits)."""
+    H, nb, _ = mask.shape
+    nq = (nb * block_size + 127) // 128
+    per_col = block_size // 64
+    cap = nb * per_col
+    if kv_tiles is None:
+        kv_tiles = cap
+    counts = np.zeros((H, nq), dtype=np.int32)
+    lists: List[List[List[int]]] = []
+    for h in range(H):
+        hl = []
+        for t in range(nq):
+            ent = []
+            if block_size == 64:
+                r0, r1 = 2 * t, 2 * t + 1
+                for j in range(nb):
+                    m0 = bool(mask[h, r0, j]) if r0 < nb else False
+                    m1 = bool(mask[h, r1, j]) if r1 < nb else False
+                    if m0 or m1:
+                        bits = 3 if union_rows else (int(m0) | (int(m1) << 1))
+                        if j < kv_tiles:
+                            ent.append((j << 2) | bits)
+            else:
+                for j in range(nb):
+                    if mask[h, t, j]:
+                        for s in range(2):
+                            if 2 * j + s < kv_tiles:
+                                ent.append(((2 * j + s) << 2) | 3)
+            counts[h, t] = len(ent)
+            hl.append(ent)
+        lists.append(hl)
+    return counts, lists
+
+
+def token_mask_from_tiles(lists, H: int, q_len: int, kv_len: int) -> np.ndarray:
+    """Token-level (H, q_len, kv_len) mask the block-sparse kernel realises."""
+    m = np.zeros((H, q_len, kv_len), dtype=bool)
+    for h in range(H):
+        for t, ent in enumerate(lists[h]):
+            for e in ent:
+                kt, bits = e >> 2, e & 3
+                k0, k1 = kt * 64, min(kt * 64 + 64, kv_len)
+                for half in range(2):
+                    if bits & (1 << half):
+                        q0 = t * 128 + 64 * half
+                        q1 = min(q0 + 64, q_len)
+                        if q0 < q1:
+                            m[h, q0:q1, k0:k1] = True
+    return m
+
+
+def token_mask_from_blocks(mask: np.ndarray, block_size: int) -> np.ndarray:
+    """Expand an (H, nb, nb) block mask to tokens."""
+    return np.repeat(np.repeat(mask, block_size, axis=1), block_size, axis=2)
+
+
+# --------------------------------------------------------------------------------------
+# attention and the sparsity map
+# --------------------------------------------------------------------------------------
+def masked_attention(q, k, v, token_mask: Optional[np.ndarray] = None, scale=None,
+                     dtype=np.float32):
+    """Softmax attention under a token mask; rows with no allowed key give 0 / -inf LSE.
+
+    q, k, v: (H, S, D) (one batch element). Returns (out (H,Sq,D), lse (H,Sq)) in `dtype`.
+    Textbook definition (MoD/mod/triton_flash_sparsity.py:346-370 without the map).
+    """
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    v = np.asarray(v, dtype=dtype)
+    D = q.shape[-1]
+    if scale is None:
+        scale = D ** -0.5
+    s = np.einsum("hqd,hkd->hqk", q, k).astype(dtype) * dtype(scale)
+    if token_mask is not None:
+        s = np.where(token_mask, s, -np.inf)
+    m = s.max(axis=-1, keepdims=True)
+    empty = ~np.isfinite(m)
+    m = np.where(empty, 0, m)
+    p = np.exp(s - m)
+    l = p.sum(axis=-1, keepdims=True)
+    out = np.einsum("hqk,hkd->hqd", p, v) / np.where(l > 0, l, 1)
+    out = np.where(l > 0, out, 0)
+    with np.errstate(divide="ignore"):
+        lse = np.where(l[..., 0] > 0, np.log(np.where(l[..., 0] > 0, l[..., 0], 1)) + m[..., 0], -np.inf)
+    return out.astype(dtype), lse.astype(dtype)
+
+
+def probability_map(q, k, threshold: float, block_size: int, q_off: int, k_off: int,
+                    video_tokens: int) -> np.ndarray:
+    """fp32 probability map: mean over each block of [softmax < threshold].
+
+    tests/test_flash_sparsity.py:28-49 and triton_flash_sparsity.py:346-370 of the
+    reference. q, k: (H, S, D).
+    """
+    q = np.asarray(q, dtype=np.float32)
+    k = np.asarray(k, dtype=np.float32)
+    H, S, D = q.shape
+    s = np.einsum("hqd,hkd->hqk", q, k) * np.float32(D ** -0.5)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p = p / p.sum(axis=-1, keepdims=True)
+    pv = p[:, q_off:q_off + video_tokens, k_off:k_off + video_tokens]
+    nb = video_tokens // block_size
+    blk = (pv < threshold).reshape(H, nb, block_size, nb, block_size)
+    return blk.mean(axis=(2, 4)).astype(np.float32)
+
+
+def replay_map(q, k, lse, *, scale: float, log_threshold: float, q_off: int, k_off: int,
+               video_blocks: int, block_size: int, dtype: str = "bf16") -> np.ndarray:
+    """Replayed fp16 map (MoD/mod/cuda_flash_sparsity_kernel.cu:82-163).
+
+    q*scale is formed in fp32 and rounded to the input dtype (:86-92), scores are exact
+    dot products (fp64, which equals the fp32 accumulation whenever that is exact, e.g.
+    for dyadic inputs), the comparison is strict against fp32(lse + log_threshold)
+    (:138-143), and the ratio count/bs^2 is rounded to fp16 (:158-163).
+    q, k: (H, S, D) float values already representable in `dtype`; lse: (H, S).
+    """
+    rnd = bf16_round if dtype == "bf16" else fp16_round
+    q = np.asarray(q, dtype=np.float32)
+    k = np.asarray(k, dtype=np.float32)
+    H = q.shape[0]
+    vt = video_blocks * block_size
+    qs = rnd(q[:, q_off:q_off + vt] * np.float32(scale)).astype(np.float64)
+    kk = k[:, k_off:k_off + vt].astype(np.float64)
+    thr = (np.asarray(lse, dtype=np.float32)[:, q_off:q_off + vt] + np.float32(log_threshold)).astype(np.float32)
+    out = np.zeros((H, video_blocks, video_blocks), dtype=np.float16)
+    for h in range(H):
+        s = qs[h] @ kk[h].T
+        below = s < thr[h][:, None].astype(np.float64)
+        cnt = below.reshape(video_blocks, block_size, video_blocks, block_size).sum(axis=(1, 3))
+        out[h] = (cnt.astype(np.float32) / np.float32(block_size * block_size)).astype(np.float16)
+    return out
+
+
+def refresh_merge(prev: np.ndarray, cur: np.ndarray, mask: np.ndarray) -> np.ndarray:
+    """torch.where(mask == False, prev, cur) (MoD/mod/attn_mask.py:671-675)."""
+    return np.where(mask, cur, prev)
+
+
+# --------------------------------------------------------------------------------------
+# schedule (MoD/mod/attn_mask.py:598-712 with the processors' use_dense gate)
+# --------------------------------------------------------------------------------------
+def step_phase(step: int, W: int, T: int) -> str:
+    """Phase of one call: 'dense' | 'map_fit' | 'map_fit_predict' | 'refresh' | 'sparse'.
+
+    Processors run dense below W-2 (hunyuan/attention_processor.py:110-115); W-2 maps and
+    fits (zero features); W-1 maps, fits and predicts; after W a refresh happens when
+    (step-W) % T == T-1, otherwise the sparse engine runs.
+    """
+    if step < W - 2:
+        return "dense"
+    if step < W - 1:
+        return "map_fit"
+    if step == W - 1:
+        return "map_fit_predict"
+    if (step - W) % T == T - 1:
+        return "refresh"
+    return "sparse"

@@ -1,0 +1,346 @@
+"""Parity of every HIP kernel with the CPU oracle (GPU only).
+
+Tolerances: integer/byte/index outputs are compared bit-exactly; attention outputs use
+the north-star bound (max-abs <= 2e-2, mean-abs <= 2e-3 against fp32/fp64 attention on
+the same bf16/fp16-rounded inputs and the same effective mask); map counts use the
+reference test bounds (<= 2.1 counts per block against the same-LSE replay,
+tests/test_flash_sparsity.py:100-101, and <= 8.1 against the fp32 probability map,
+:138-139).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import mod_dit_amd as md
+import oracle as O
+from mod_dit_amd import ops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _randn(shape, seed, dtype, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype).to(DEV)
+
+
+def _check_attn(out, ref, tag=""):
+    err = np.abs(_np(out).astype(np.float64) - ref)
+    print(f"{tag} max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
+    assert err.max() <= 2e-2, tag
+    assert err.mean() <= 2e-3, tag
+
+
+# ====================================================================== dense attention
+@pytest.mark.parametrize("H,S,D,dtype", [
+    (2, 4096, 64, torch.bfloat16),    # configs[0] plumbing shape
+    (2, 1000, 128, torch.bfloat16),   # ragged tail (1000 = 7*128 + 104)
+    (1, 640, 128, torch.float16),
+    (3, 200, 64, torch.float16),
+])
+def test_flash_fwd_matches_fp64(H, S, D, dtype):
+    q, k, v = (_randn((1, H, S, D), 100 + i, dtype) for i in range(3))
+    out, lse = ops.flash_fwd(q, k, v)
+    torch.cuda.synchronize()
+    ref, ref_lse = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), None, dtype=np.float64)
+    _check_attn(out[0], ref, f"dense H={H} S={S} D={D} {dtype}")
+    np.testing.assert_allclose(_np(lse[0]), ref_lse, rtol=0, atol=2e-3)
+
+
+def test_flash_fwd_strided_view_and_cross_lengths():
+    B, H, S, D = 1, 2, 384, 128
+    store = _randn((B, S, H, D), 7, torch.bfloat16)  # (B,S,H,D) storage
+    q = store.transpose(1, 2)                          # (B,H,S,D) view, non-contiguous
+    k = _randn((B, H, 700, D), 8, torch.bfloat16)
+    v = _randn((B, H, 700, D), 9, torch.bfloat16)
+    out, lse = ops.flash_fwd(q, k, v)
+    ref, _ = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), None, dtype=np.float64)
+    _check_attn(out[0], ref, "strided q, Skv=700")
+    out2, _ = ops.flash_fwd(q.contiguous(), k, v)
+    assert torch.equal(out, out2)
+
+
+# ====================================================================== tiles + sparse
+def _random_block_mask(H, nb, density, seed, diag=True):
+    rng = np.random.default_rng(seed)
+    m = rng.random((H, nb, nb)) < density
+    if diag:
+        m[:, np.arange(nb), np.arange(nb)] = True
+    return m
+
+
+def _tiles_np(t: ops.TileList):
+    c = t.counts.cpu().numpy()
+    e = t.entries.cpu().numpy()
+    return c, [[list(e[h, i, :c[h, i]]) for i in range(c.shape[1])] for h in range(c.shape[0])]
+
+
+@pytest.mark.parametrize("union", [False, True])
+@pytest.mark.parametrize("nb,bs", [(64, 64), (13, 64), (9, 128)])
+def test_mask_to_tiles_bit_exact(nb, bs, union):
+    m = _random_block_mask(3, nb, 0.4, nb + bs)
+    tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=union)
+    c, lists = _tiles_np(tiles)
+    rc, rlists = O.tiles_from_mask(m, bs, union)
+    assert np.array_equal(c, rc)
+    assert lists == rlists
+
+
+@pytest.mark.parametrize("union", [False, True])
+def test_block_sparse_config1_matches_masked_fp64(union):
+    # B=1, H=2, N=4096, d=64, 64x64 blocks, 50% random mask, diagonal on
+    H, S, D, bs = 2, 4096, 64, 64
+    q, k, v = (_randn((1, H, S, D), 200 + i, torch.bfloat16) for i in range(3))
+    m = _random_block_mask(H, S // bs, 0.5, 5)
+    tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=union)
+    out, lse = ops.block_sparse_fwd(q, k, v, tiles, return_lse=True)
+    _, lists = _tiles_np(tiles)
+    tm = O.token_mask_from_tiles(lists, H, S, S)
+    if not union:
+        assert np.array_equal(tm, O.token_mask_from_blocks(m, bs))
+    ref, ref_lse = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), tm, dtype=np.float64)
+    _check_attn(out[0], ref, f"sparse config1 union={union}")
+    np.testing.assert_allclose(_np(lse[0]), ref_lse, rtol=0, atol=2e-3)
+
+
+def test_block_sparse_all_true_equals_dense_and_empty_rows_are_zero():
+    H, S, D, bs = 2, 512, 128, 64
+    q, k, v = (_randn((1, H, S, D), 300 + i, torch.bfloat16) for i in range(3))
+    nb = S // bs
+    full = torch.ones((H, nb, nb), dtype=torch.bool, device=DEV)
+    t_full = ops.mask_to_tiles(full, bs, union_rows=False)
+    o_sparse, _ = ops.block_sparse_fwd(q, k, v, t_full)
+    o_dense, _ = ops.flash_fwd(q, k, v, return_lse=False)
+    assert torch.equal(o_sparse, o_dense)
+    m = full.clone()
+    m[:, 3, :] = False  # rows 192..255 have no key block
+    t = ops.mask_to_tiles(m, bs, union_rows=False)
+    o, lse = ops.block_sparse_fwd(q, k, v, t, return_lse=True)
+    assert torch.all(o[:, :, 192:256] == 0)
+    assert torch.all(torch.isneginf(lse[:, :, 192:256]))
+
+
+def test_block_sparse_bs128_mask():
+    H, S, D, bs = 2, 1024, 128, 128
+    q, k, v = (_randn((1, H, S, D), 400 + i, torch.bfloat16) for i in range(3))
+    m = _random_block_mask(H, S // bs, 0.3, 11)
+    tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs)
+    out, _ = ops.block_sparse_fwd(q, k, v, tiles)
+    ref, _ = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), O.token_mask_from_blocks(m, bs),
+                                dtype=np.float64)
+    _check_attn(out[0], ref, "sparse bs128")
+
+
+# ====================================================================== sparsity map
+def _layout(model_type, bs):
+    # tests/test_flash_sparsity.py:22-25
+    if model_type == "wan":
+        return bs * 2, bs * 2, 0
+    return bs * 3, bs * 2, bs
+
+
+@pytest.mark.parametrize("model_type", ["hunyuan", "cogvideox", "wan"])
+@pytest.mark.parametrize("bs", [64, 128])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_sparsity_map_dyadic_bit_exact(model_type, bs, D, dtype):
+    S, vt, tt = _layout(model_type, bs)
+    rng = np.random.default_rng(bs + D)
+    qn = rng.integers(-4, 5, size=(2, 2, S, D)).astype(np.float32) / 8
+    kn = rng.integers(-4, 5, size=(2, 2, S, D)).astype(np.float32) / 8
+    q = torch.from_numpy(qn).to(dtype).to(DEV)
+    k = torch.from_numpy(kn).to(dtype).to(DEV)
+    scale = D ** -0.5
+    s = np.einsum("bhqd,bhkd->bhqk", qn.astype(np.float64), kn.astype(np.float64)) * scale
+    lse = np.log(np.exp(s).sum(-1)).astype(np.float32)
+    vb, qo, ko = O.video_layout(model_type, S, vt, tt, bs)
+    ln_thr = math.log(1e-3)
+    got = md.cuda_sparsity_map(q, k, torch.from_numpy(lse).to(DEV), softmax_scale=scale,
+                               log_threshold=ln_thr, q_video_offset=qo, k_video_offset=ko,
+                               video_blocks=vb, block_size=bs)
+    assert got.dtype == torch.float16 and got.shape == (2, 2, vb, vb)
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    for b in range(2):
+        ref = O.replay_map(qn[b], kn[b], lse[b], scale=scale, log_threshold=ln_thr, q_off=qo,
+                           k_off=ko, video_blocks=vb, block_size=bs, dtype=dt)
+        assert np.array_equal(got[b].cpu().numpy(), ref), (model_type, bs, D, dtype, b)
+
+
+@pytest.mark.parametrize("bs", [64, 128])
+@pytest.mark.parametrize("D", [64, 128])
+def test_sparsity_map_randn_within_reference_count_bound(bs, D):
+    # the reference's CUDA-vs-Triton bound (<= 2.1 counts) against the same-LSE replay
+    torch.manual_seed(7)
+    S = bs * 4
+    q = torch.randn(2, 2, S, D).to(torch.bfloat16)
+    k = torch.randn(2, 2, S, D).to(torch.bfloat16)
+    scale = D ** -0.5
+    sq = (q.float() * scale).to(torch.bfloat16).float()
+    lse = torch.logsumexp(sq @ k.float().transpose(-1, -2), dim=-1)
+    got = md.cuda_sparsity_map(q.to(DEV), k.to(DEV), lse.to(DEV), softmax_scale=scale,
+                               log_threshold=math.log(1e-3), q_video_offset=0, k_video_offset=0,
+                               video_blocks=S // bs, block_size=bs)
+    for b in range(2):
+        ref = O.replay_map(q[b].float().numpy(), k[b].float().numpy(), lse[b].numpy(),
+                           scale=scale, log_threshold=math.log(1e-3), q_off=0, k_off=0,
+                           video_blocks=S // bs, block_size=bs)
+        err = np.abs(got[b].cpu().float().numpy() - ref.astype(np.float32)) * bs * bs
+        assert err.max() <= 2.1
+    g = got.float()
+    assert torch.all((g >= 0) & (g <= 1))
+
+
+@pytest.mark.parametrize("model_type", ["hunyuan", "cogvideox", "wan"])
+@pytest.mark.parametrize("bs", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_public_api_matches_probability_reference(model_type, bs, dtype):
+    # tests/test_flash_sparsity.py:107-139
+    torch.manual_seed(11)
+    S, vt, tt = _layout(model_type, bs)
+    q = torch.randn(1, 2, S, 64).to(dtype)
+    k = torch.randn_like(q)
+    v = torch.randn_like(q)
+    out, sp = md.flash_attn_with_sparsity_map(q.to(DEV), k.to(DEV), v.to(DEV), 1e-3, bs,
+                                              model_type=model_type,
+                                              video_token_num=vt if model_type != "wan" else 0,
+                                              text_token_num=tt)
+    assert out.shape == q.shape
+    _, qo, ko = O.video_layout(model_type, S, vt, tt, bs)
+    ref = O.probability_map(q[0].float().numpy(), k[0].float().numpy(), 1e-3, bs, qo, ko, vt)
+    err = np.abs(sp[0].cpu().float().numpy() - ref) * bs * bs
+    assert err.max() <= 8.1
+    ref_o, _ = O.masked_attention(q[0].float().numpy(), k[0].float().numpy(), v[0].float().numpy(),
+                                  None, dtype=np.float64)
+    _check_attn(out[0], ref_o, "map pass output")
+
+
+def test_non_positive_threshold_produces_zero_map():
+    q = torch.randn(1, 1, 128, 64).to(torch.float16).to(DEV)
+    out, sp = md.flash_attn_with_sparsity_map(q, q, q, 0.0, 64, model_type="wan")
+    assert out.shape == q.shape
+    assert torch.count_nonzero(sp).item() == 0
+
+
+def test_kernels_use_current_stream():
+    q = torch.randn(1, 1, 128, 64).to(torch.float16).to(DEV)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        out, sp = md.flash_attn_with_sparsity_map(q, q, q, 1e-3, 64, model_type="wan")
+        marker = sp.float().sum() + out.float().sum()
+    stream.synchronize()
+    assert torch.isfinite(marker)
+
+
+# ====================================================================== M^T S / solve
+@pytest.mark.parametrize("n,bpf", [(64, 16), (100, 7), (1800, 60)])
+def test_mts_bit_exact_on_map_domain(n, bpf):
+    H = 2 if n > 500 else 3
+    rng = np.random.default_rng(n)
+    S = (rng.integers(0, 4097, size=(H, n, n)) / 4096.0).astype(np.float16)
+    got = md.compute_mts(torch.from_numpy(S).to(DEV), bpf).cpu().numpy()
+    assert np.array_equal(got, O.mts_exact(S, bpf))
+    if n <= 100:
+        loop = O.mts_loop(S, bpf)  # the reference's fp32 order: diag/col sums are exact
+        assert np.array_equal(got[:, :-1], loop[:, :-1])
+
+
+def test_mts_arbitrary_fp16_and_fp32_inputs():
+    rng = np.random.default_rng(3)
+    n, bpf = 37, 5
+    bits = rng.integers(0, 0x7C00, size=(2, n, n)).astype(np.uint16)
+    bits |= (rng.integers(0, 2, size=bits.shape) << 15).astype(np.uint16)
+    S = bits.view(np.float16)
+    got = md.compute_mts(torch.from_numpy(S.copy()).to(DEV), bpf).cpu().numpy()
+    assert np.array_equal(got, O.mts_exact(S, bpf))
+    S32 = rng.normal(size=(2, n, n)).astype(np.float32)
+    got32 = md.compute_mts(torch.from_numpy(S32).to(DEV), bpf).cpu().numpy()
+    want = np.stack([O.moddit_ref._mts_f64(S32[h].astype(np.float64), bpf) for h in range(2)])
+    np.testing.assert_allclose(got32, want, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("n,bpf", [(64, 16), (270, 21)])
+def test_solve_lstsq_matches_fp64_ridge(n, bpf):
+    rng = np.random.default_rng(n)
+    H = 3
+    S = (rng.integers(0, 4097, size=(H, n, n)) / 4096.0).astype(np.float16)
+    st = md.create_adaptive_mask_state("wan", H, n * 64, 0, bpf * 64, n // bpf, block_size=64)
+    feats = md.solve_lstsq(st, torch.from_numpy(S).to(DEV), step=st["warmup_steps"], blocks_per_frame=bpf,
+                           regularization=1.0)
+    X = O.ridge_solve(S.astype(np.float64), bpf, 1.0)
+    got = feats["_x"].cpu().numpy().astype(np.float64)
+    scale = np.abs(X).max()
+    print(f"solve n={n}: max rel err {np.abs(got - X).max() / scale:.3e}", flush=True)
+    assert np.abs(got - X).max() <= 1e-4 * scale
+    f = O.features_from_x(got.astype(np.float32), n)
+    assert np.array_equal(feats["c"].cpu().numpy(), f["c"])
+    zero = md.solve_lstsq(st, torch.from_numpy(S).to(DEV), step=st["warmup_steps"] - 2, blocks_per_frame=bpf)
+    assert torch.count_nonzero(zero["_x"]).item() == 0
+
+
+# ====================================================================== select / modes
+@pytest.mark.parametrize("n,k", [(8, 5), (64, 40), (1800, 400), (10, 1000)])
+def test_select_lines_bit_exact(n, k):
+    rng = np.random.default_rng(n + k)
+    H = 4
+    xc = rng.normal(size=(H, 3 * n)).astype(np.float32)
+    xl = rng.normal(size=(H, 3 * n)).astype(np.float32)
+    # inject exact ties, signed zeros and NaN
+    xc[0, :6] = 0.5
+    xl[0, :6] = 0.5
+    xc[1, 3], xl[1, 3] = np.nan, 0.0
+    xc[2, 2 * n - 1:2 * n + 3] = 0.0
+    xl[2, 2 * n - 1:2 * n + 3] = -0.0
+    got = ops.select_lines(torch.from_numpy(xc).to(DEV), torch.from_numpy(xl).to(DEV), n, 10, k)
+    ref = O.choose_topk_lines(xc, xl, n, 10, k)
+    assert np.array_equal(got.cpu().numpy(), ref)
+
+
+def test_check_bd():
+    x = torch.zeros(4, 9, device=DEV)
+    x[:, -1] = torch.tensor([0.5, 1.0, 1.5, -3.0], device=DEV)
+    mode = torch.tensor([0, 0, 0, 2], dtype=torch.uint8, device=DEV)
+    ops.check_bd(x, mode, 1.0)
+    assert mode.tolist() == [1, 1, 0, 2]
+
+
+# ====================================================================== mask from lines
+@pytest.mark.parametrize("model_type", ["wan", "hunyuan", "cogvideox", "other"])
+@pytest.mark.parametrize("bs", [64, 128])
+@pytest.mark.parametrize("union", [False, True])
+def test_mask_from_lines_bit_exact(model_type, bs, union):
+    rng = np.random.default_rng(hash((model_type, bs, union)) % 2**32)
+    H, n, bpf, k = 5, 23, 4, 7
+    tb = 3 if model_type in ("hunyuan", "cogvideox") else 0
+    nb = n + tb
+    sel = rng.integers(0, 3 * n - 1, size=(H, k)).astype(np.int32)
+    modes = np.array([0, 1, 2, 0, 1], np.uint8)
+    st = {"block_size": bs, "text_token_num": tb * bs, "video_token_num": n * bs,
+          "model_type": model_type, "tile_rows": "union" if union else "exact"}
+    mask, tiles = md.attn_mask._generate_mask_and_tiles(
+        st, H, nb * bs, bpf, torch.from_numpy(sel).to(DEV),
+        torch.from_numpy(modes).to(DEV), torch.device(DEV))
+    ref = O.generate_mask_from_lines(sel, list(modes), seq_len=nb * bs, block_size=bs,
+                                     video_tokens=n * bs, text_tokens=tb * bs, bpf=bpf,
+                                     model_type=model_type)
+    got = mask.cpu().numpy()
+    assert got.shape == ref.shape and np.array_equal(got, ref)
+    c, lists = _tiles_np(tiles)
+    rc, rlists = O.tiles_from_mask(ref, bs, union)
+    assert np.array_equal(c, rc) and lists == rlists
+
+
+def test_refresh_merge_exact():
+    rng = np.random.default_rng(9)
+    H, n = 3, 50
+    prev = rng.random((H, n, n)).astype(np.float16)
+    cur = rng.random((H, n, n)).astype(np.float16)
+    full = rng.random((H, n + 4, n + 4)) < 0.5
+    mask = torch.from_numpy(full).to(DEV)[:, :n, :n]  # strided view like the hunyuan slice
+    got = ops.refresh_merge(torch.from_numpy(prev).to(DEV), torch.from_numpy(cur).to(DEV), mask)
+    assert np.array_equal(got.cpu().numpy(), O.refresh_merge(prev, cur, full[:, :n, :n]))

@@ -1,0 +1,136 @@
+"""Host-side checks that need no GPU: the C-ABI library, validation, state, modes."""
+import ctypes
+import re
+import types
+
+import numpy as np
+import pytest
+import torch
+
+import mod_dit_amd as md
+import oracle as O
+from mod_dit_amd import _lib
+
+HEADER = _lib.LIB_PATH.parents[1] / "include" / "moddit.h"
+
+
+def _declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(moddit_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_symbols()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_lib.EXPORTED)
+    assert lib.moddit_version().startswith(b"moddit-mi355x")
+
+
+def test_mtm_host_matches_oracle_closed_form_and_brute_force():
+    for n, bpf in [(4, 2), (9, 4), (64, 16)]:
+        got = md.compute_mtm(n, bpf, 1.0).numpy()
+        assert np.array_equal(got, O.mtm_closed_form(n, bpf, 1.0))
+    M = O.build_M(9, 4)
+    assert np.array_equal(md.compute_mtm(9, 4, 0.5).numpy(), M.T @ M + 0.5 * np.eye(27))
+
+
+def test_c_abi_rejects_bad_arguments_before_any_launch():
+    lib = _lib.load()
+    rc = lib.moddit_mtm_host(0, 1, 1.0, None)
+    assert rc == _lib.MODDIT_EINVAL
+    assert b"mtm" in lib.moddit_last_error()
+    s = _lib.strides3(0, 0, 0)
+    rc = lib.moddit_flash_fwd(16, 16, 16, 16, None, 1, 1, 64, 64, 96, s, s, s, s, 0.1, 0, None)
+    assert rc == _lib.MODDIT_EUNSUPPORTED and b"head_dim" in lib.moddit_last_error()
+    rc = lib.moddit_sparsity_map(16, 16, 16, 16, 1, 1, 128, 64, s, s, 0.1, -1.0, 0, 0, 2, 32, 0, None)
+    assert rc == _lib.MODDIT_EINVAL and b"block_size" in lib.moddit_last_error()
+    rc = lib.moddit_select_lines(16, 16, 1, 6000, 10, 5, 16, None)
+    assert rc == _lib.MODDIT_EINVAL and b"exceeds" in lib.moddit_last_error()
+    rc = lib.moddit_mask_from_lines(16, 1, 1, 16, 4, 2, _lib.LAYOUT_WAN, 5, 0, 64, 1,
+                                    None, None, None, 0, 0, None)
+    assert rc == _lib.MODDIT_EINVAL and b"nb == n" in lib.moddit_last_error()
+    with pytest.raises(_lib.ModditError, match="mtm"):
+        _lib.check(lib.moddit_mtm_host(-1, 1, 1.0, None), "moddit_mtm_host")
+
+
+def test_state_matches_reference_fields_and_errors():
+    st = md.create_adaptive_mask_state("wan", 40, 69120, 512, 3840, 18, block_size=64)
+    assert st["blocks_per_frame"] == 60 and st["threshold"] == 1.5e-4
+    assert st["features_history"] is None and st["mask"] is None
+    assert st["tile_rows"] == "union"
+    assert not md.is_warmup_complete(st)
+    with pytest.raises(ValueError, match="not support"):
+        md.create_adaptive_mask_state("wan", 1, 64, 0, 64, 1, sparse_type="bogus")
+
+
+class _FakeCuda:
+    """Duck-typed stand-in carrying only what _validate_inputs reads."""
+
+    def __init__(self, shape, dtype=torch.float16, is_cuda=True):
+        self.shape = torch.Size(shape)
+        self.ndim = len(shape)
+        self.dtype = dtype
+        self.is_cuda = is_cuda
+        self.device = torch.device("cuda", 0)
+
+
+# the reference's test_input_validation cases (tests/test_flash_sparsity.py:178-201)
+@pytest.mark.parametrize(
+    "mutation,error_type,match",
+    [
+        ({"block_size": 32}, ValueError, "block_size"),
+        ({"video_token_num": 65}, ValueError, "divisible"),
+        ({"model_type": "unknown"}, ValueError, "Unknown model_type"),
+        ({"threshold": float("nan")}, ValueError, "NaN"),
+    ],
+)
+def test_input_validation(mutation, error_type, match):
+    q = _FakeCuda((1, 1, 128, 64))
+    args = dict(query=q, key=q, value=q, threshold=1e-3, block_size=64, model_type="hunyuan",
+                video_token_num=64, text_token_num=64)
+    args.update(mutation)
+    with pytest.raises(error_type, match=match):
+        md._validate_inputs(**args)
+
+
+def test_input_validation_more_cases():
+    q = _FakeCuda((1, 1, 128, 64))
+    with pytest.raises(TypeError, match="float16 or bfloat16"):
+        f = _FakeCuda((1, 1, 128, 64), dtype=torch.float32)
+        md._validate_inputs(f, f, f, 1e-3, 64, "wan", 0, 0)
+    with pytest.raises(ValueError, match="CUDA tensors"):
+        c = _FakeCuda((1, 1, 128, 64), is_cuda=False)
+        md._validate_inputs(c, c, c, 1e-3, 64, "wan", 0, 0)
+    with pytest.raises(ValueError, match="head_dim"):
+        d = _FakeCuda((1, 1, 128, 96))
+        md._validate_inputs(d, d, d, 1e-3, 64, "wan", 0, 0)
+    with pytest.raises(ValueError, match="exceed"):
+        md._validate_inputs(q, q, q, 1e-3, 64, "hunyuan", 128, 64)
+    thr, vb, qo, ko = md._validate_inputs(q, q, q, 1e-3, 64, "cogvideox", 64, 64)
+    assert (vb, qo, ko) == (1, 64, 64)
+    assert md._validate_inputs(q, q, q, 0.0, 64, "wan", 0, 0)[:2] == (0.0, 2)
+
+
+def test_head_modes_reads_like_reference_list():
+    hm = md.HeadModes(torch.tensor([0, 1, 2, 0], dtype=torch.uint8))
+    assert list(hm) == ["sparse", "block_diagonal", "full", "sparse"]
+    assert hm == ["sparse", "block_diagonal", "full", "sparse"]
+    assert len(hm) == 4 and hm[1] == "block_diagonal"
+
+
+def test_check_bd_values_host_form():
+    vals = torch.tensor([[0.0, 2.0], [0.0, 1.0], [0.0, 0.5]])
+    assert md.check_bd_values(vals, ["sparse"] * 3, threshold=1) == ["sparse", "block_diagonal",
+                                                                     "block_diagonal"]
+
+
+def test_product_path_refuses_cpu_tensors():
+    with pytest.raises(ValueError, match="GPU"):
+        md.ops.compute_mts(torch.zeros(1, 4, 4, dtype=torch.float16), 2)
+    st = md.create_adaptive_mask_state("wan", 1, 256, 0, 128, 2, block_size=64)
+    with pytest.raises(ValueError, match="GPU"):
+        md.solve_lstsq(st, torch.zeros(1, 4, 4, dtype=torch.float16), 11, 2)

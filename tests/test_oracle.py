@@ -1,0 +1,280 @@
+"""Pins the CPU oracle against closed forms, brute force and invariants (CPU only).
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped term, a wrong
+sign or index, a transposed operand) fails it; none of them retypes the oracle's own
+formula.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+
+# ------------------------------------------------------------------ line model -------
+@pytest.mark.parametrize("n,bpf", [(3, 1), (4, 2), (7, 3), (8, 4), (9, 4), (12, 5)])
+def test_mtm_closed_form_equals_explicit_MtM(n, bpf):
+    M = O.build_M(n, bpf)
+    lam = 1.0
+    assert np.array_equal(O.mtm_closed_form(n, bpf, lam), M.T @ M + lam * np.eye(3 * n))
+
+
+def test_build_M_counts():
+    # every cell sits on exactly one diagonal and one column
+    n, bpf = 6, 2
+    M = O.build_M(n, bpf)
+    nd = 2 * n - 1
+    assert np.all(M[:, :nd].sum(axis=1) == 1)
+    assert np.all(M[:, nd:nd + n].sum(axis=1) == 1)
+    assert M[:, -1].sum() == (n // bpf) * bpf * bpf
+
+
+def _dyadic_map(rng, H, n, bs=64):
+    counts = rng.integers(0, bs * bs + 1, size=(H, n, n))
+    return (counts / float(bs * bs)).astype(np.float16)
+
+
+@pytest.mark.parametrize("n,bpf", [(5, 2), (16, 4), (17, 5)])
+def test_mts_exact_equals_brute_force(n, bpf):
+    rng = np.random.default_rng(0)
+    S = _dyadic_map(rng, 3, n)
+    M = O.build_M(n, bpf)
+    brute = np.stack([M.T @ S[h].astype(np.float64).ravel() for h in range(3)])
+    got = O.mts_exact(S, bpf)
+    assert np.array_equal(got.astype(np.float64), brute.astype(np.float32).astype(np.float64))
+
+
+def test_mts_exact_arbitrary_fp16_is_correctly_rounded():
+    # arbitrary-signed fp16 values incl. subnormals: exact sum, one rounding
+    rng = np.random.default_rng(1)
+    n, bpf = 9, 3
+    bits = rng.integers(0, 0x7C00, size=(2, n, n)).astype(np.uint16)
+    bits |= (rng.integers(0, 2, size=bits.shape) << 15).astype(np.uint16)
+    S = bits.view(np.float16)
+    from fractions import Fraction
+
+    got = O.mts_exact(S, bpf)
+    M = O.build_M(n, bpf)
+    for h in range(2):
+        vals = [Fraction(float(x)) for x in S[h].ravel()]
+        for f in [0, n, 2 * n - 2, 2 * n - 1 + 3, 3 * n - 1]:
+            exact = sum(v for v, w in zip(vals, M[:, f]) if w)
+            assert got[h, f] == np.float32(float(exact))  # float(Fraction) is correctly rounded
+
+
+@pytest.mark.parametrize("n,bpf", [(6, 2), (10, 3)])
+def test_mts_loop_equals_exact_on_map_domain(n, bpf):
+    rng = np.random.default_rng(2)
+    S = _dyadic_map(rng, 2, n)
+    loop = O.mts_loop(S, bpf)
+    exact = O.mts_exact(S, bpf)
+    # diagonal and column sums are exact in fp32 for map-domain values
+    assert np.array_equal(loop[:, :-1], exact[:, :-1])
+    np.testing.assert_allclose(loop[:, -1], exact[:, -1], rtol=1e-6)
+
+
+def test_ridge_solve_recovers_planted_features():
+    n, bpf, lam = 8, 2, 1.0
+    rng = np.random.default_rng(3)
+    xstar = rng.normal(size=(2, 3 * n))
+    M = O.build_M(n, bpf)
+    S = np.stack([(M @ xstar[h]).reshape(n, n) for h in range(2)])
+    X = O.ridge_solve(S, bpf, lam)
+    G = M.T @ M + lam * np.eye(3 * n)
+    want = np.linalg.solve(G, (M.T @ M) @ xstar.T).T
+    np.testing.assert_allclose(X, want, rtol=1e-9, atol=1e-9)
+    # normal equations: (M^T M + lam I) X = M^T S
+    res = G @ X.T - np.stack([M.T @ S[h].ravel() for h in range(2)]).T
+    assert np.abs(res).max() < 1e-9
+    # S = 0 -> X = 0
+    assert np.all(O.ridge_solve(np.zeros((1, n, n)), bpf, lam) == 0)
+
+
+def test_reconstruct_is_M_times_X():
+    n, bpf = 7, 3
+    rng = np.random.default_rng(4)
+    X = rng.normal(size=(2, 3 * n))
+    M = O.build_M(n, bpf)
+    rec = O.reconstruct_map(X, n, bpf)
+    for h in range(2):
+        np.testing.assert_allclose(rec[h].ravel(), M @ X[h], rtol=1e-12)
+
+
+def test_features_slicing_halves_columns():
+    n = 5
+    X = np.arange(2 * 3 * n, dtype=np.float32).reshape(2, 3 * n)
+    f = O.features_from_x(X, n)
+    assert np.array_equal(f["d"], X[:, :2 * n - 1])
+    assert np.array_equal(f["c"] * 2, X[:, 2 * n - 1:3 * n - 1])
+    assert np.array_equal(f["b_d"], X[:, -1])
+
+
+# ------------------------------------------------------------------ selection --------
+def test_first_prediction_is_cur_times_one_plus_inv_T():
+    # at W-1 the previous features are zeros (MoD/mod/cuda_lstsq.py:265-270)
+    n, T = 6, 10
+    rng = np.random.default_rng(5)
+    xc = rng.normal(size=(2, 3 * n)).astype(np.float32)
+    v = O.predict_lines(xc, np.zeros_like(xc), n, T)
+    c = xc[:, 2 * n - 1:3 * n - 1] / 2
+    np.testing.assert_allclose(v[:, :n], c * (1 + 1 / T), rtol=1e-6)
+    np.testing.assert_allclose(v[:, n:], xc[:, :2 * n - 1] * (1 + 1 / T), rtol=1e-6)
+
+
+def test_choose_topk_matches_sorted_order_with_ties_nan_and_signed_zero():
+    n, T, k = 5, 3, 6
+    xc = np.zeros((1, 3 * n), np.float32)
+    xl = np.zeros((1, 3 * n), np.float32)
+    # craft predictions directly through cur with last = cur (pred = cur)
+    vals = np.array([0.5, -1.0, 0.5, np.nan, -0.0, 0.0, 2.0, -1.0, 3.0, 0.5, 0.25, 0.0, 7.0, -5.0],
+                    dtype=np.float32)
+    nd = 2 * n - 1
+    # v[:n] = X[nd:nd+n]/2, v[n:] = X[:nd]
+    xc[0, nd:nd + n] = vals[:n] * 2
+    xc[0, :nd] = vals[n:n + nd]
+    xl[:] = xc
+    got = O.choose_topk_lines(xc, xl, n, T, k)[0]
+    keyed = sorted(range(len(vals)), key=lambda i: (math.isnan(vals[i]), 0.0 if vals[i] == 0 else vals[i], i))
+    assert list(got) == sorted(keyed[:k])
+
+
+# ------------------------------------------------------------------ mask -------------
+@pytest.mark.parametrize("seed", range(4))
+def test_generate_mask_restatement_equals_cell_definition(seed):
+    rng = np.random.default_rng(10 + seed)
+    n, bpf, H, k = 11, 3, 4, 5
+    sel = rng.integers(0, 3 * n - 1, size=(H, k))
+    modes = [O.MODE_SPARSE, O.MODE_BLOCK_DIAGONAL, O.MODE_FULL, O.MODE_SPARSE]
+    m = O.generate_mask_from_lines(sel, modes, seq_len=n * 64, block_size=64,
+                                   video_tokens=n * 64, text_tokens=0, bpf=bpf, model_type="wan")
+    for h in range(H):
+        for i in range(n):
+            for j in range(n):
+                assert m[h, i, j] == O.mask_cell(sel[h], modes[h], n, bpf, i, j)
+
+
+def test_generate_mask_layouts():
+    n, bpf, bs = 4, 2, 64
+    sel = np.array([[0], [n + (n - 1)]])  # head 0: column 0; head 1: main diagonal
+    modes = [O.MODE_SPARSE, O.MODE_SPARSE]
+    hy = O.generate_mask_from_lines(sel, modes, seq_len=(n + 2) * bs, block_size=bs,
+                                    video_tokens=n * bs, text_tokens=2 * bs, bpf=bpf,
+                                    model_type="hunyuan")
+    assert hy.shape == (2, n + 2, n + 2)
+    assert hy[:, n:, :].all() and hy[:, :, n:].all()
+    assert hy[0, :n, 0].all() and not hy[0, :n, 1:n].any()
+    assert np.array_equal(hy[1, :n, :n], np.eye(n, dtype=bool))
+    cg = O.generate_mask_from_lines(sel, modes, seq_len=(n + 2) * bs, block_size=bs,
+                                    video_tokens=n * bs, text_tokens=2 * bs, bpf=bpf,
+                                    model_type="cogvideox")
+    assert cg[:, :2, :].all() and cg[:, :, :2].all()
+    assert np.array_equal(cg[1, 2:, 2:], np.eye(n, dtype=bool))
+    other = O.generate_mask_from_lines(sel, modes, seq_len=n * bs, block_size=bs,
+                                       video_tokens=n * bs, text_tokens=0, bpf=bpf,
+                                       model_type="unknown")
+    assert other.all()
+
+
+def test_block_diagonal_covers_partial_last_frame():
+    # i // bpf == j // bpf also holds in the tail past the last full frame (:535-539)
+    n, bpf = 5, 2
+    m = O.generate_mask_from_lines(np.full((1, 1), 10**6), [O.MODE_BLOCK_DIAGONAL], seq_len=n * 64,
+                                   block_size=64, video_tokens=n * 64, text_tokens=0, bpf=bpf,
+                                   model_type="wan")
+    assert m[0, 4, 4] and not m[0, 3, 4]
+
+
+# ------------------------------------------------------------------ tiles ------------
+@pytest.mark.parametrize("nb,bs", [(7, 64), (8, 64), (3, 128)])
+def test_tiles_realise_the_mask(nb, bs):
+    rng = np.random.default_rng(20 + nb)
+    mask = rng.random((2, nb, nb)) < 0.4
+    L = nb * bs
+    counts, exact = O.tiles_from_mask(mask, bs, union_rows=False)
+    tm = O.token_mask_from_tiles(exact, 2, L, L)
+    assert np.array_equal(tm, O.token_mask_from_blocks(mask, bs))
+    _, union = O.tiles_from_mask(mask, bs, union_rows=True)
+    tu = O.token_mask_from_tiles(union, 2, L, L)
+    assert (tu | ~tm).all()  # union is a superset
+    if bs == 64:
+        # union == OR of the two rows of each pair (MoD/mod/attn_mask.py:299-303)
+        for t in range((nb + 1) // 2):
+            rows = mask[:, 2 * t:2 * t + 2].any(axis=1)
+            assert np.array_equal(tu[:, t * 128, ::64], rows)
+    for h in range(2):
+        for t in range(counts.shape[1]):
+            keys = [e >> 2 for e in exact[h][t]]
+            assert keys == sorted(keys) and len(keys) == counts[h, t]
+
+
+# ------------------------------------------------------------------ attention / map --
+def test_masked_attention_all_true_is_dense_and_local_is_blockwise():
+    rng = np.random.default_rng(30)
+    H, S, D = 2, 128, 16
+    q, k, v = (rng.normal(size=(H, S, D)).astype(np.float32) for _ in range(3))
+    dense, lse = O.masked_attention(q, k, v, None, dtype=np.float64)
+    full, lse_full = O.masked_attention(q, k, v, np.ones((H, S, S), bool), dtype=np.float64)
+    np.testing.assert_allclose(full, dense, rtol=1e-12)
+    # brute force softmax
+    s = np.einsum("hqd,hkd->hqk", q.astype(np.float64), k.astype(np.float64)) / math.sqrt(D)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    np.testing.assert_allclose(dense, (p / p.sum(-1, keepdims=True)) @ v, rtol=1e-10)
+    np.testing.assert_allclose(lse, np.log(np.exp(s).sum(-1)), rtol=1e-10)
+    # block-diagonal (64) mask = independent attention per block
+    bm = O.token_mask_from_blocks(np.eye(2, dtype=bool)[None].repeat(H, 0), 64)
+    loc, _ = O.masked_attention(q, k, v, bm, dtype=np.float64)
+    for b in range(2):
+        sl = slice(64 * b, 64 * b + 64)
+        ref, _ = O.masked_attention(q[:, sl], k[:, sl], v[:, sl], None, dtype=np.float64)
+        np.testing.assert_allclose(loc[:, sl], ref, rtol=1e-10)
+    # a row with no allowed key gives zeros and -inf LSE
+    em = np.ones((H, S, S), bool)
+    em[:, 3] = False
+    out, l = O.masked_attention(q, k, v, em, dtype=np.float64)
+    assert np.all(out[:, 3] == 0) and np.all(np.isneginf(l[:, 3]))
+
+
+def test_probability_map_zero_threshold_is_zero():
+    # reference known answer: tests/test_flash_sparsity.py:142-154
+    rng = np.random.default_rng(31)
+    q = rng.normal(size=(1, 128, 64)).astype(np.float32)
+    m = O.probability_map(q, q, 0.0, 64, 0, 0, 128)
+    assert np.count_nonzero(m) == 0
+
+
+def test_replay_equals_probability_map_on_dyadic_inputs():
+    # d=64 -> scale 1/8 exact; q,k in {-4..4}/8 -> bf16-exact scaled q and exact scores;
+    # LSE from exact softmax; cells are equal when no score sits at the threshold
+    rng = np.random.default_rng(32)
+    H, S, D, bs, thr = 2, 256, 64, 64, 1e-3
+    q = rng.integers(-4, 5, size=(H, S, D)).astype(np.float32) / 8
+    k = rng.integers(-4, 5, size=(H, S, D)).astype(np.float32) / 8
+    s = np.einsum("hqd,hkd->hqk", q.astype(np.float64), k.astype(np.float64)) / 8
+    lse = np.log(np.exp(s).sum(-1))
+    assert np.abs(s - (lse[..., None] + math.log(thr))).min() > 1e-5
+    rep = O.replay_map(q, k, lse.astype(np.float32), scale=1 / 8, log_threshold=math.log(thr),
+                       q_off=0, k_off=0, video_blocks=S // bs, block_size=bs)
+    prob = O.probability_map(q, k, thr, bs, 0, 0, S)
+    np.testing.assert_array_equal(rep.astype(np.float32), prob.astype(np.float16).astype(np.float32))
+
+
+def test_replay_rounds_count_ratio_to_fp16():
+    # 64x64 blocks: ratios are multiples of 2^-12; counts >= 2048 lose their last bit
+    r = (np.arange(0, 4097) / 4096.0).astype(np.float32).astype(np.float16).astype(np.float64)
+    assert np.all(r[:2049] * 4096 == np.arange(2049))
+    assert np.all((r * 4096) % 1 == 0)
+
+
+def test_bf16_round_half_to_even():
+    x = np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -1.0 - 2 ** -8], np.float32)
+    np.testing.assert_array_equal(O.bf16_round(x), np.array([1.0, 1.0 + 2 ** -6, -1.0], np.float32))
+
+
+# ------------------------------------------------------------------ schedule ---------
+def test_step_schedule_W12_T10():
+    phases = [O.step_phase(s, 12, 10) for s in range(50)]
+    assert phases[:10] == ["dense"] * 10
+    assert phases[10] == "map_fit" and phases[11] == "map_fit_predict"
+    assert [s for s, p in enumerate(phases) if p == "refresh"] == [21, 31, 41]
+    assert phases.count("sparse") == 50 - 12 - 3
