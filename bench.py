@@ -142,6 +142,19 @@ def mask_overhead_once(art, *, bpf, block_size, union):
                         nb=n, text_blocks=0, block_size=block_size, union_rows=union)
 
 
+def measured_traffic(name="attention_hunyuan_headline.md"):
+    """HBM bytes per sparse-attention launch from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch"):
+                    return int(line.split(":")[1].split()[0]), f"profiles/{name}"
+    except OSError:
+        pass
+    return None, None
+
+
 def time_events(fn, reps):
     """Per-call durations (ms) from HIP events on torch's current stream."""
     out = []
@@ -219,6 +232,9 @@ def main(argv=None):
     ap.add_argument("--threshold", type=float, default=1e-4)
     ap.add_argument("--dense-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile", choices=("sparse", "dense", "replay", "mask", "copy"), default=None,
+                    help="run only the named kernel(s) after setup (for rocprofv3 counter passes); "
+                         "prints no JSON")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -229,6 +245,17 @@ def main(argv=None):
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+
+    if args.profile == "copy":
+        # calibration for HBM byte counters: a plain device copy of a known size
+        nbytes = 1 << 30
+        src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").normal_()
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {nbytes} bytes x {args.steps}")
+        return 0
 
     cfg = CONFIGS[args.config]
     H, F, Hp, Wp, D = cfg["H"], cfg["F"], cfg["Hp"], cfg["Wp"], cfg["D"]
@@ -256,6 +283,23 @@ def main(argv=None):
 
     def sparse_call():
         ops.block_sparse_fwd(q, k, v, tiles, out=out)
+
+    if args.profile is not None:
+        for _ in range(args.steps):
+            if args.profile == "sparse":
+                sparse_call()
+            elif args.profile == "dense":
+                ops.flash_fwd(q, k, v, return_lse=False, out=out)
+            elif args.profile == "replay":
+                _, lse_p = ops.flash_fwd(q, k, v, return_lse=True, out=out)
+                ops.sparsity_map(q, k, lse_p, softmax_scale=D ** -0.5,
+                                 log_threshold=math.log(args.threshold), q_video_offset=0,
+                                 k_video_offset=0, video_blocks=N // bs, block_size=bs)
+            elif args.profile == "mask":
+                mask_overhead_once(art, bpf=bpf, block_size=bs, union=union)
+        torch.cuda.synchronize()
+        log(f"profile {args.profile}: {args.steps} calls done")
+        return 0
 
     for _ in range(args.warmup):
         sparse_call()
@@ -299,6 +343,7 @@ def main(argv=None):
         cpu = cpu_baseline(q, k, v, tiles)
 
     achieved = exec_flop / (kernel_ms * 1e-3) / 1e12
+    traffic, traffic_src = measured_traffic() if args.config == "hunyuan" else (None, None)
     result = {
         "metric": "block-sparse attn effective TFLOP/s + ms/call at 115k tokens, 83% sparsity",
         "value": round(eff_flop / (ms * 1e-3) / 1e12, 3),
@@ -336,7 +381,9 @@ def main(argv=None):
             "peak": MI355X_BF16_DENSE_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / MI355X_BF16_DENSE_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1)",
+            "traffic_source": traffic_src,
             "kernel": "attention_fwd_kernel<128, Bf16, sparse>",
             "kernel_ms": round(kernel_ms, 4),
         },
