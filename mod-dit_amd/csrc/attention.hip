@@ -32,8 +32,8 @@ constexpr int kThreads = 256;
 
 template <int D>
 struct AttnLds {
-  static constexpr int kPitchK = D * 2 + 16;  // bytes per K row
-  static constexpr int kPitchV = kBN * 2 + 8;  // bytes per V^T row
+  static constexpr int kPitchK = D * 2 + 16;  // bytes per K row (68 dwords for d=128: 4 mod 64 banks)
+  static constexpr int kPitchV = kBN * 2 + 16;  // bytes per V^T row (36 dwords: 16 lanes hit 16 bank quads)
   static constexpr int kKBytes = kBN * kPitchK;
   static constexpr int kVBytes = D * kPitchV;
   static constexpr int kStage = kKBytes + kVBytes;
@@ -61,15 +61,28 @@ struct AttnParams {
   int cap;
 };
 
-template <int D, typename E, bool kSparse>
+// Rows of a 64-key tile are stored in LDS in the order pi(r): inside every 16-row chunk
+// the row groups [4,8) and [8,12) are swapped. With that order the S^T accumulator of
+// lane half h holds keys 8h..8h+7 of each 16-key chunk, in order, so the matching V^T
+// operand is one 16-byte LDS read.
+__device__ __forceinline__ int key_perm(int r) { return r ^ ((((r >> 2) ^ (r >> 3)) & 1) * 12); }
+
+// The running row max is only moved when a tile's max exceeds it by more than this many
+// log2 units; probabilities then stay <= 2^8 and the O rescale is skipped for whole
+// waves on most tiles. Softmax is shift-invariant, so results do not depend on it.
+constexpr float kRescaleSlack = 8.0f;
+
+template <int D, typename E, bool kSparse, bool kRagged>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p) {
   using L = AttnLds<D>;
   using V8 = typename E::vec8;
-  constexpr int kDChunks = D / 16;       // MFMA k-steps over d for S^T
-  constexpr int kDSub = D / 32;          // 32-row blocks of O^T
-  constexpr int kVecPerRow = D / 8;      // 16-byte vectors per token row
-  constexpr int kKVecs = kBN * kVecPerRow / kThreads;  // K vectors per thread
-  constexpr int kKeysPerGroup = D / 32;  // V keys per thread (x 8 dims)
+  constexpr int kDChunks = D / 16;                       // MFMA k-steps over d for S^T
+  constexpr int kDSub = D / 32;                          // 32-row blocks of O^T
+  constexpr int kVecPerRow = D / 8;                      // 16-byte vectors per token row
+  constexpr int kKVecs = kBN * kVecPerRow / kThreads;    // K vectors per thread
+  constexpr int kKRowStep = kThreads / kVecPerRow;       // K rows between a thread's vectors
+  constexpr int kKeysPerThr = D / 32;                    // V keys per thread (x 8 dims)
+  constexpr int kKeyGroups = kBN / kKeysPerThr;          // V key groups per tile
 
   extern __shared__ __align__(16) unsigned char smem[];
 
@@ -113,50 +126,65 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
   }
 
   // ---- global -> register staging of one K/V tile ----
+  // K: thread owns column k_col of rows k_row0 + i*kKRowStep (row-major, 256 B rows).
+  // V: thread owns keys v_kgrp*kKeysPerThr + j, dims v_dgrp*8.. (transposed into LDS).
+  const int k_col = tid % kVecPerRow;
+  const int k_row0 = tid / kVecPerRow;
+  const int v_kgrp = tid % kKeyGroups;
+  const int v_dgrp = tid / kKeyGroups;
+  const uint16_t* k_thr = kb + static_cast<int64_t>(k_row0) * p.k_ss + k_col * 8;
+  const uint16_t* v_thr = vb + static_cast<int64_t>(v_kgrp * kKeysPerThr) * p.v_ss + v_dgrp * 8;
+  const int64_t k_tile_stride = static_cast<int64_t>(kBN) * p.k_ss;
+  const int64_t v_tile_stride = static_cast<int64_t>(kBN) * p.v_ss;
   u32x4 kreg[kKVecs];
-  u32x4 vreg[kKeysPerGroup];
-  const int v_dgrp = tid % (D / 8);
-  const int v_kgrp = tid / (D / 8);
+  u32x4 vreg[kKeysPerThr];
 
-#define MODDIT_LOAD_TILE(KT)                                                        \
-  do {                                                                              \
-    const int key0_ = (KT) * kBN;                                                   \
-    _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_) {                         \
-      const int vec_ = tid + i_ * kThreads;                                         \
-      int key_ = key0_ + vec_ / kVecPerRow;                                         \
-      key_ = key_ < p.kv_len ? key_ : p.kv_len - 1;                                 \
-      kreg[i_] = reinterpret_cast<const u32x4*>(kb + key_ * p.k_ss)[vec_ % kVecPerRow]; \
-    }                                                                               \
-    _Pragma("unroll") for (int j_ = 0; j_ < kKeysPerGroup; ++j_) {                  \
-      int key_ = key0_ + v_kgrp * kKeysPerGroup + j_;                               \
-      key_ = key_ < p.kv_len ? key_ : p.kv_len - 1;                                 \
-      vreg[j_] = reinterpret_cast<const u32x4*>(vb + key_ * p.v_ss)[v_dgrp];        \
-    }                                                                               \
+#define MODDIT_LOAD_TILE(KT)                                                              \
+  do {                                                                                    \
+    if constexpr (!kRagged) {                                                             \
+      const uint16_t* kp_ = k_thr + (KT) * k_tile_stride;                                 \
+      _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_)                               \
+          kreg[i_] = *reinterpret_cast<const u32x4*>(kp_ + i_ * kKRowStep * p.k_ss);      \
+      const uint16_t* vp_ = v_thr + (KT) * v_tile_stride;                                 \
+      _Pragma("unroll") for (int j_ = 0; j_ < kKeysPerThr; ++j_)                          \
+          vreg[j_] = *reinterpret_cast<const u32x4*>(vp_ + j_ * p.v_ss);                  \
+    } else {                                                                              \
+      const int key0_ = (KT) * kBN;                                                       \
+      _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_) {                             \
+        int key_ = key0_ + k_row0 + i_ * kKRowStep;                                       \
+        key_ = key_ < p.kv_len ? key_ : p.kv_len - 1;                                     \
+        kreg[i_] = *reinterpret_cast<const u32x4*>(kb + key_ * p.k_ss + k_col * 8);       \
+      }                                                                                   \
+      _Pragma("unroll") for (int j_ = 0; j_ < kKeysPerThr; ++j_) {                        \
+        int key_ = key0_ + v_kgrp * kKeysPerThr + j_;                                     \
+        key_ = key_ < p.kv_len ? key_ : p.kv_len - 1;                                     \
+        vreg[j_] = *reinterpret_cast<const u32x4*>(vb + key_ * p.v_ss + v_dgrp * 8);      \
+      }                                                                                   \
+    }                                                                                     \
   } while (0)
 
-#define MODDIT_STORE_TILE(STAGE)                                                    \
-  do {                                                                              \
-    unsigned char* ks_ = smem + (STAGE) * L::kStage;                                \
-    unsigned char* vs_ = ks_ + L::kKBytes;                                          \
-    _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_) {                         \
-      const int vec_ = tid + i_ * kThreads;                                         \
-      *reinterpret_cast<u32x4*>(ks_ + (vec_ / kVecPerRow) * L::kPitchK +            \
-                                (vec_ % kVecPerRow) * 16) = kreg[i_];               \
-    }                                                                               \
-    /* V^T: dim (v_dgrp*8 + dd), keys v_kgrp*kKeysPerGroup + 0.. */                 \
-    _Pragma("unroll") for (int dd_ = 0; dd_ < 8; ++dd_) {                           \
-      unsigned char* dst_ =                                                         \
-          vs_ + (v_dgrp * 8 + dd_) * L::kPitchV + v_kgrp * kKeysPerGroup * 2;       \
-      if constexpr (kKeysPerGroup == 4) {                                           \
-        u32x2 w_;                                                                   \
-        w_.x = pack2(u16_at(vreg[0], dd_), u16_at(vreg[1], dd_));                   \
-        w_.y = pack2(u16_at(vreg[2], dd_), u16_at(vreg[3], dd_));                   \
-        *reinterpret_cast<u32x2*>(dst_) = w_;                                       \
-      } else {                                                                      \
-        *reinterpret_cast<uint32_t*>(dst_) =                                        \
-            pack2(u16_at(vreg[0], dd_), u16_at(vreg[1], dd_));                      \
-      }                                                                             \
-    }                                                                               \
+#define MODDIT_STORE_TILE(STAGE)                                                          \
+  do {                                                                                    \
+    unsigned char* ks_ = smem + (STAGE) * L::kStage;                                      \
+    unsigned char* vs_ = ks_ + L::kKBytes;                                                \
+    _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_) {                               \
+      const int row_ = key_perm(k_row0 + i_ * kKRowStep);                                 \
+      *reinterpret_cast<u32x4*>(ks_ + row_ * L::kPitchK + k_col * 16) = kreg[i_];         \
+    }                                                                                     \
+    _Pragma("unroll") for (int dd_ = 0; dd_ < 8; ++dd_) {                                 \
+      unsigned char* dst_ =                                                               \
+          vs_ + (v_dgrp * 8 + dd_) * L::kPitchV + v_kgrp * kKeysPerThr * 2;               \
+      const uint32_t sel_ = (dd_ & 1) ? 0x07060302u : 0x05040100u;                        \
+      if constexpr (kKeysPerThr == 4) {                                                   \
+        u32x2 w_;                                                                         \
+        w_.x = __builtin_amdgcn_perm(vreg[1][dd_ >> 1], vreg[0][dd_ >> 1], sel_);         \
+        w_.y = __builtin_amdgcn_perm(vreg[3][dd_ >> 1], vreg[2][dd_ >> 1], sel_);         \
+        *reinterpret_cast<u32x2*>(dst_) = w_;                                             \
+      } else {                                                                            \
+        *reinterpret_cast<uint32_t*>(dst_) =                                              \
+            __builtin_amdgcn_perm(vreg[1][dd_ >> 1], vreg[0][dd_ >> 1], sel_);            \
+      }                                                                                   \
+    }                                                                                     \
   } while (0)
 
   f32x16 oacc[kDSub];
@@ -201,7 +229,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
       const unsigned char* ks = smem + (it & 1) * L::kStage;
       const unsigned char* vs = ks + L::kKBytes;
 
-      // S^T = K . Q^T, two 32-key halves.
+      // S^T = K . Q^T, two 32-key halves (rows in key_perm order).
       f32x16 s0 = f32x16{};
       f32x16 s1 = f32x16{};
 #pragma unroll
@@ -213,13 +241,15 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
         s1 = E::mma(a1, qf[c], s1);
       }
 
-      const int key0 = kt * kBN;
-      if (key0 + kBN > p.kv_len) {
+      if constexpr (kRagged) {
+        const int key0 = kt * kBN;
+        if (key0 + kBN > p.kv_len) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kr = 8 * (i >> 2) + 4 * half + (i & 3);
-          if (key0 + kr >= p.kv_len) s0[i] = -INFINITY;
-          if (key0 + 32 + kr >= p.kv_len) s1[i] = -INFINITY;
+          for (int i = 0; i < 16; ++i) {
+            const int kr = (i >> 3) * 16 + 8 * half + (i & 7);  // actual key of acc row i
+            if (key0 + kr >= p.kv_len) s0[i] = -INFINITY;
+            if (key0 + 32 + kr >= p.kv_len) s1[i] = -INFINITY;
+          }
         }
       }
 
@@ -229,10 +259,18 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s1[i]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mxs = mx * p.scale_log2;
 
-      const float m_new = fmaxf(m_run, mx * p.scale_log2);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      const bool need = mxs > m_run + kRescaleSlack;
+      if (__ballot(need) != 0ull) {
+        const float m_new = need ? mxs : m_run;
+        const float alpha = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+        l_run *= alpha;
+#pragma unroll
+        for (int dsub = 0; dsub < kDSub; ++dsub) oacc[dsub] *= alpha;
+        m_run = m_new;
+      }
+      const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
 
       V8 pb[4];
       float rs = 0.f;
@@ -244,19 +282,16 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
         pb[i >> 3][i & 7] = static_cast<typename E::elem>(e0);
         pb[2 + (i >> 3)][i & 7] = static_cast<typename E::elem>(e1);
       }
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
+      l_run += rs;
 
+      // O^T += V^T . P^T: lane half h supplies keys 8h..8h+7 of each 16-key chunk.
 #pragma unroll
       for (int dsub = 0; dsub < kDSub; ++dsub) {
-        oacc[dsub] *= alpha;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const unsigned char* row = vs + (dsub * 32 + c32) * L::kPitchV + c * 32 + half * 8;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
-          const u32x4 a = {lo.x, lo.y, hi.x, hi.y};
-          oacc[dsub] = E::mma(as_vec8<V8>(a), pb[c], oacc[dsub]);
+          const V8 a = *reinterpret_cast<const V8*>(vs + (dsub * 32 + c32) * L::kPitchV + c * 32 +
+                                                    half * 16);
+          oacc[dsub] = E::mma(a, pb[c], oacc[dsub]);
         }
       }
     }
@@ -293,10 +328,10 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
 #undef MODDIT_LOAD_TILE
 #undef MODDIT_STORE_TILE
 
-template <int D, typename E, bool kSparse>
-int launch_attention(const AttnParams& p, int batch, hipStream_t stream) {
+template <int D, typename E, bool kSparse, bool kRagged>
+int launch_attention_impl(const AttnParams& p, int batch, hipStream_t stream) {
   using L = AttnLds<D>;
-  auto kernel = attention_fwd_kernel<D, E, kSparse>;
+  auto kernel = attention_fwd_kernel<D, E, kSparse, kRagged>;
   static bool configured = false;  // the attribute is per function, same on every device
   if (!configured) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -316,6 +351,13 @@ int launch_attention(const AttnParams& p, int batch, hipStream_t stream) {
                      stream, p);
   MODDIT_CHECK_LAUNCH("attention");
   return MODDIT_OK;
+}
+
+template <int D, typename E, bool kSparse>
+int launch_attention(const AttnParams& p, int batch, hipStream_t stream) {
+  // Key counts that are a multiple of the tile need no clamping or masking at all.
+  if (p.kv_len % kBN == 0) return launch_attention_impl<D, E, kSparse, false>(p, batch, stream);
+  return launch_attention_impl<D, E, kSparse, true>(p, batch, stream);
 }
 
 int attention_entry(const void* q, const void* k, const void* v, void* o, float* lse, int batch,
