@@ -59,6 +59,8 @@ struct AttnParams {
   const int32_t* counts;
   const int32_t* entries;
   int cap;
+  uint32_t k_bytes;  // byte span of one head's K rows [0, kv_len)
+  uint32_t v_bytes;
 };
 
 // Rows of a 64-key tile are stored in LDS in the order pi(r): inside every 16-row chunk
@@ -123,6 +125,11 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
     const u32x4* src = reinterpret_cast<const u32x4*>(qb + r * p.q_ss);
 #pragma unroll
     for (int c = 0; c < kDChunks; ++c) qf[c] = as_vec8<V8>(src[2 * c + half]);
+    // Sparse: retire the Q loads here, otherwise the waitcnt pass keeps them pending
+    // across the loop back-edge and every tile's first MFMAs wait for the K/V prefetch.
+    // Dense: measured faster without it (the in-order wait de-phases the two waves that
+    // share a SIMD), so it is left to the compiler there.
+    if constexpr (kSparse) __builtin_amdgcn_s_waitcnt(0);
   }
 
   // ---- global -> register staging of one K/V tile ----
@@ -132,34 +139,37 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
   const int k_row0 = tid / kVecPerRow;
   const int v_kgrp = tid % kKeyGroups;
   const int v_dgrp = tid / kKeyGroups;
-  const uint16_t* k_thr = kb + static_cast<int64_t>(k_row0) * p.k_ss + k_col * 8;
-  const uint16_t* v_thr = vb + static_cast<int64_t>(v_kgrp * kKeysPerThr) * p.v_ss + v_dgrp * 8;
-  const int64_t k_tile_stride = static_cast<int64_t>(kBN) * p.k_ss;
-  const int64_t v_tile_stride = static_cast<int64_t>(kBN) * p.v_ss;
+  // Buffer resources over this head's K/V rows; the byte span was checked on the host.
+  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kb, p.k_bytes);
+  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vb, p.v_bytes);
+  const uint32_t k_voff = static_cast<uint32_t>((k_row0 * p.k_ss + k_col * 8) * 2);
+  const uint32_t v_voff = static_cast<uint32_t>((v_kgrp * kKeysPerThr * p.v_ss + v_dgrp * 8) * 2);
+  const uint32_t k_row_step = static_cast<uint32_t>(kKRowStep * p.k_ss * 2);
+  const uint32_t k_tile_bytes = static_cast<uint32_t>(kBN * p.k_ss * 2);
+  const uint32_t v_row_bytes = static_cast<uint32_t>(p.v_ss * 2);
+  const uint32_t v_tile_bytes = static_cast<uint32_t>(kBN * p.v_ss * 2);
   u32x4 kreg[kKVecs];
   u32x4 vreg[kKeysPerThr];
 
+  // Full tiles put the tile offset in the SGPR offset (loop-invariant VGPR offsets keep
+  // the loads free of register reuse hazards); the ragged variant puts it in the
+  // range-checked VGPR offset so rows past kv_len read as zeros.
 #define MODDIT_LOAD_TILE(KT)                                                              \
   do {                                                                                    \
     if constexpr (!kRagged) {                                                             \
-      const uint16_t* kp_ = k_thr + (KT) * k_tile_stride;                                 \
+      const uint32_t kso_ = static_cast<uint32_t>(KT) * k_tile_bytes;                     \
+      const uint32_t vso_ = static_cast<uint32_t>(KT) * v_tile_bytes;                     \
       _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_)                               \
-          kreg[i_] = *reinterpret_cast<const u32x4*>(kp_ + i_ * kKRowStep * p.k_ss);      \
-      const uint16_t* vp_ = v_thr + (KT) * v_tile_stride;                                 \
+          kreg[i_] = buf_load16(k_rsrc, k_voff, kso_ + i_ * k_row_step);                  \
       _Pragma("unroll") for (int j_ = 0; j_ < kKeysPerThr; ++j_)                          \
-          vreg[j_] = *reinterpret_cast<const u32x4*>(vp_ + j_ * p.v_ss);                  \
+          vreg[j_] = buf_load16(v_rsrc, v_voff, vso_ + j_ * v_row_bytes);                 \
     } else {                                                                              \
-      const int key0_ = (KT) * kBN;                                                       \
-      _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_) {                             \
-        int key_ = key0_ + k_row0 + i_ * kKRowStep;                                       \
-        key_ = key_ < p.kv_len ? key_ : p.kv_len - 1;                                     \
-        kreg[i_] = *reinterpret_cast<const u32x4*>(kb + key_ * p.k_ss + k_col * 8);       \
-      }                                                                                   \
-      _Pragma("unroll") for (int j_ = 0; j_ < kKeysPerThr; ++j_) {                        \
-        int key_ = key0_ + v_kgrp * kKeysPerThr + j_;                                     \
-        key_ = key_ < p.kv_len ? key_ : p.kv_len - 1;                                     \
-        vreg[j_] = *reinterpret_cast<const u32x4*>(vb + key_ * p.v_ss + v_dgrp * 8);      \
-      }                                                                                   \
+      const uint32_t kto_ = static_cast<uint32_t>(KT) * k_tile_bytes;                     \
+      const uint32_t vto_ = static_cast<uint32_t>(KT) * v_tile_bytes;                     \
+      _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_)                               \
+          kreg[i_] = buf_load16(k_rsrc, k_voff + kto_ + i_ * k_row_step, 0);              \
+      _Pragma("unroll") for (int j_ = 0; j_ < kKeysPerThr; ++j_)                          \
+          vreg[j_] = buf_load16(v_rsrc, v_voff + vto_ + j_ * v_row_bytes, 0);             \
     }                                                                                     \
   } while (0)
 
@@ -193,23 +203,24 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
   float m_run = -INFINITY;
   float l_run = 0.f;
 
-  auto tile_of = [&](int it, int& kt, int& flags) {
-    if (kSparse) {
-      // Entries come from the tile-list builders; clamp anyway so a corrupt list can
-      // only select a wrong (in-bounds) tile, never address outside K/V.
-      const int e = list[it];
-      kt = e >> 2;
-      kt = kt < 0 ? 0 : (kt < p.n_ktiles ? kt : p.n_ktiles - 1);
-      flags = e & 3;
-    } else {
-      kt = it;
-      flags = 3;
-    }
+  // Tile-list entries are uniform; decode with a clamp so a corrupt list can only select
+  // a wrong (in-bounds) tile, never address outside K/V.
+  auto decode = [&](int e_raw, int& kt, int& flags) {
+    const int e = __builtin_amdgcn_readfirstlane(e_raw);
+    kt = e >> 2;
+    kt = kt < 0 ? 0 : (kt < p.n_ktiles ? kt : p.n_ktiles - 1);
+    flags = e & 3;
+  };
+  auto entry = [&](int i) -> int {
+    return kSparse ? list[i] : ((i << 2) | 3);
   };
 
+  int e_cur = 0, e_next = 0;
   if (n_iter > 0) {
+    e_cur = entry(0);
+    if (n_iter > 1) e_next = entry(1);
     int kt0, fl0;
-    tile_of(0, kt0, fl0);
+    decode(e_cur, kt0, fl0);
     MODDIT_LOAD_TILE(kt0);
     MODDIT_STORE_TILE(0);
   }
@@ -217,11 +228,15 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
 
   for (int it = 0; it < n_iter; ++it) {
     int kt, flags;
-    tile_of(it, kt, flags);
+    decode(e_cur, kt, flags);
     const bool has_next = it + 1 < n_iter;
+    int e_after = 0;
     if (has_next) {
+      // The entry two tiles ahead is requested before this tile's K/V loads, so waiting
+      // for it later never waits for those loads.
+      if (it + 2 < n_iter) e_after = entry(it + 2);
       int kn, fn;
-      tile_of(it + 1, kn, fn);
+      decode(e_next, kn, fn);
       MODDIT_LOAD_TILE(kn);
     }
 
@@ -298,6 +313,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
 
     if (has_next) MODDIT_STORE_TILE((it + 1) & 1);
     __syncthreads();
+    e_cur = e_next;
+    e_next = e_after;
   }
 
   // ---- epilogue ----
@@ -420,6 +437,17 @@ int attention_entry(const void* q, const void* k, const void* v, void* o, float*
     set_error("attention: kv_len must be positive");
     return MODDIT_EINVAL;
   }
+  // Per-head K/V spans are addressed with 32-bit buffer offsets; a whole 64-key tile past
+  // the last row must also stay below 2^31.
+  const int64_t k_span = (static_cast<int64_t>(kv_len) - 1) * ks[2] * 2 + head_dim * 2;
+  const int64_t v_span = (static_cast<int64_t>(kv_len) - 1) * vs[2] * 2 + head_dim * 2;
+  const int64_t max_off = (static_cast<int64_t>(p.n_ktiles) * kBN) * (ks[2] > vs[2] ? ks[2] : vs[2]) * 2;
+  if (k_span > 0x7fffffffLL || v_span > 0x7fffffffLL || max_off > 0x7fffffffLL) {
+    set_error("attention: one head's K/V span exceeds 2 GiB of 32-bit offsets");
+    return MODDIT_EUNSUPPORTED;
+  }
+  p.k_bytes = static_cast<uint32_t>(k_span);
+  p.v_bytes = static_cast<uint32_t>(v_span);
 
   hipStream_t st = as_stream(stream);
   const bool bf = dtype == MODDIT_BF16;

@@ -104,6 +104,23 @@ __device__ __forceinline__ uint16_t u16_at(const u32x4& v, int i) {
 }
 
 // ---------------------------------------------------------------------------------
+// Buffer loads. A raw buffer resource covers one tensor slice; offsets are 32-bit
+// bytes. The VGPR offset (plus the instruction offset) is range-checked against
+// `bytes`: out-of-range 16-byte loads return zeros instead of touching memory. The
+// SGPR offset is not range-checked, so it may only carry offsets known to be in range.
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                            uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                       r, static_cast<int>(voff), static_cast<int>(soff), 0));
+}
+
+// ---------------------------------------------------------------------------------
 // Workgroup -> tile mapping that keeps consecutive tiles on one XCD.
 // The dispatcher hands workgroup w to XCD (w % 8); remapping makes XCD x own one
 // contiguous range of logical tiles so tiles that share K/V share that XCD's L2.

@@ -48,6 +48,7 @@ struct ReplayParams {
   int n_ktiles;  // 64-key tiles of the video region
   float scale;
   float log_thr;
+  uint32_t k_bytes;  // byte span of one head's video K rows
 };
 
 template <int D, typename E>
@@ -98,28 +99,31 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
       qf[c] = as_vec8<V8>(packed);
     }
     thr = p.lse[static_cast<int64_t>(bh) * p.seq_len + r] + p.log_thr;
+    // Retire these loads before the loop (see attention.hip).
+    __builtin_amdgcn_s_waitcnt(0);
   }
 
+  // K rows of the video region through a buffer resource (loop-invariant VGPR offsets,
+  // tile offset in the SGPR offset: every tile is a full in-range tile).
+  const int k_col = tid % kVecPerRow;
+  const int k_row0 = tid / kVecPerRow;
+  constexpr int kKRowStep = kThreads / kVecPerRow;
+  const uint16_t* kvid = kb + static_cast<int64_t>(p.k_off) * p.k_ss;
+  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kvid, p.k_bytes);
+  const uint32_t k_voff = static_cast<uint32_t>((k_row0 * p.k_ss + k_col * 8) * 2);
+  const uint32_t k_row_step = static_cast<uint32_t>(kKRowStep * p.k_ss * 2);
+  const uint32_t k_tile_bytes = static_cast<uint32_t>(kBN * p.k_ss * 2);
   u32x4 kreg[kKVecs];
   auto load_tile = [&](int kt) {
-    const int key0 = p.k_off + kt * kBN;
+    const uint32_t so = static_cast<uint32_t>(kt) * k_tile_bytes;
 #pragma unroll
-    for (int i = 0; i < kKVecs; ++i) {
-      const int vec = tid + i * kThreads;
-      const int row = vec / kVecPerRow;
-      const int col = vec % kVecPerRow;
-      kreg[i] = reinterpret_cast<const u32x4*>(kb + (key0 + row) * p.k_ss)[col];
-    }
+    for (int i = 0; i < kKVecs; ++i) kreg[i] = buf_load16(k_rsrc, k_voff, so + i * k_row_step);
   };
   auto store_tile = [&](int stage) {
     unsigned char* ks = smem + stage * L::kKBytes;
 #pragma unroll
-    for (int i = 0; i < kKVecs; ++i) {
-      const int vec = tid + i * kThreads;
-      const int row = vec / kVecPerRow;
-      const int col = vec % kVecPerRow;
-      *reinterpret_cast<u32x4*>(ks + row * L::kPitchK + col * 16) = kreg[i];
-    }
+    for (int i = 0; i < kKVecs; ++i)
+      *reinterpret_cast<u32x4*>(ks + (k_row0 + i * kKRowStep) * L::kPitchK + k_col * 16) = kreg[i];
   };
 
   load_tile(0);
@@ -264,6 +268,12 @@ extern "C" int moddit_sparsity_map(const void* q, const void* k, const float* ls
   p.n_ktiles = static_cast<int>(vt / kBN);
   p.scale = softmax_scale;
   p.log_thr = log_threshold;
+  const int64_t k_span = (vt - 1) * k_strides[2] * 2 + head_dim * 2;
+  if (k_span > 0x7fffffffLL) {
+    set_error("sparsity_map: one head's K span exceeds 2 GiB of 32-bit offsets");
+    return MODDIT_EUNSUPPORTED;
+  }
+  p.k_bytes = static_cast<uint32_t>(k_span);
 
   hipStream_t st = as_stream(stream);
   const bool bf = dtype == MODDIT_BF16;
