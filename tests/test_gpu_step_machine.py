@@ -1,0 +1,150 @@
+"""End-to-end schedule of SparseAttentionWithMap against the oracle (GPU only).
+
+Runs a short MOD-DiT schedule (W=4, T=3) on a wan-layout layer and checks, stage by
+stage and given identical inputs to each stage: the map against the replay oracle
+(reference count bound), the fit against the fp64 ridge solve, modes, the selected
+lines and the mask bit-exactly, the refresh merge bit-exactly, and every attention
+output against fp64 attention under the mask the kernels executed.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import mod_dit_amd as md
+import oracle as O
+from mod_dit_amd import ops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+class _Log:
+    def __init__(self):
+        self.lines = []
+
+    def isEnabledFor(self, level):
+        return True
+
+    def info(self, msg):
+        self.lines.append(msg)
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _check_attn(out, ref, tag, sparse=False):
+    """North-star bound (max-abs 2e-2, mean-abs 2e-3). Sparse rows attend to few keys, so
+    outputs can reach |o| ~ 4 where the bf16 output quantum alone is 2^-7; there the
+    elementwise bound also admits half a bf16 ulp of |ref| (2^-9 |ref|)."""
+    err = np.abs(_np(out).astype(np.float64) - ref)
+    bound = 2e-2 + (2.0 ** -9) * np.abs(ref) if sparse else 2e-2
+    assert np.all(err <= bound) and err.mean() <= 2e-3, (tag, err.max(), err.mean())
+
+
+def _structured_qkv(H, F, tpf, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    N = F * tpf
+    pos = torch.arange(N) % tpf
+    emb = torch.randn(tpf, D, generator=g) * 1.5
+    q = torch.randn(1, H, N, D, generator=g) + emb[pos]
+    k = torch.randn(1, H, N, D, generator=g) + emb[pos]
+    v = torch.randn(1, H, N, D, generator=g)
+    return (t.to(torch.bfloat16).to(DEV) for t in (q, k, v))
+
+
+@pytest.mark.parametrize("tile_rows", ["exact", "union"])
+def test_schedule_matches_oracle_stage_by_stage(tile_rows):
+    H, F, tpf, D, bs = 2, 4, 512, 64, 64
+    W, T, top_k, thr = 4, 3, 40, 1e-3
+    N = F * tpf
+    n, bpf = N // bs, tpf // bs
+    st = md.create_adaptive_mask_state("wan", H, N, 0, tpf, F, warmup_steps=W, top_k=top_k,
+                                       predict_T=T, threshold=thr, block_size=bs,
+                                       tile_rows=tile_rows)
+    log = _Log()
+    history_x = []
+    for step in range(W + 2 * T + 2):
+        q, k, v = _structured_qkv(H, F, tpf, D, seed=step)
+        qn, kn, vn = (_np(t[0]) for t in (q, k, v))
+        phase = O.step_phase(step, W, T)
+        use_dense = step < W - 2  # the processors' gate
+        prev_mask = st.get("mask")
+        prev_maps = st.get("prev_full_maps")
+        out, info = md.SparseAttentionWithMap(q, k, v, st, log, current_step=step, layer_idx=0,
+                                              use_dense=use_dense)
+        assert out.shape == q.shape
+        if phase == "dense":
+            ref, _ = O.masked_attention(qn, kn, vn, None, dtype=np.float64)
+            _check_attn(out[0], ref, f"dense step {step}")
+            assert info == {"mode": "warmup", "mask": None}
+            continue
+        if phase in ("map_fit", "map_fit_predict", "refresh"):
+            # output of a map step is the dense pass
+            ref, ref_lse = O.masked_attention(qn, kn, vn, None, dtype=np.float64)
+            _check_attn(out[0], ref, f"map-step output {step}")
+            # features: the fit of the map this step produced (or merged)
+            feats = st["features_history"][-1]
+            X = feats["_x"].cpu().numpy().astype(np.float64)
+            S_fit = st["prev_full_maps"].cpu().numpy()
+            if step == W - 2:
+                assert np.all(X == 0)  # zero features at W-2
+            else:
+                Xr = O.ridge_solve(S_fit.astype(np.float64), bpf, 1.0)
+                assert np.abs(X - Xr).max() <= 1e-4 * max(np.abs(Xr).max(), 1e-6)
+            if phase == "refresh":
+                # prev = where(mask, current map, prev) over the video blocks
+                smap = md.flash_attn_with_sparsity_map(q, k, v, thr, bs, model_type="wan")[1][0]
+                merged = O.refresh_merge(prev_maps.cpu().numpy(), smap.cpu().numpy(),
+                                         prev_mask.cpu().numpy())
+                assert np.array_equal(S_fit, merged)
+            else:
+                # the map is the replay of this step's inputs (reference count bound)
+                _, lse = ops.flash_fwd(q, k, v)
+                rep = O.replay_map(qn, kn, _np(lse[0]), scale=D ** -0.5,
+                                   log_threshold=math.log(thr), q_off=0, k_off=0,
+                                   video_blocks=n, block_size=bs)
+                err = np.abs(S_fit.astype(np.float32) - rep.astype(np.float32)) * bs * bs
+                assert err.max() <= 2.1
+        if phase in ("map_fit_predict", "refresh"):
+            hist = st["features_history"]
+            assert len(hist) == 2
+            xc, xl = (f["_x"].cpu().numpy() for f in hist[-1:] + hist[-2:-1])
+            if phase == "map_fit_predict":
+                modes = [O.MODE_BLOCK_DIAGONAL if x <= 1.0 else O.MODE_SPARSE for x in xc[:, -1]]
+                assert list(st["mode"]) == ["block_diagonal" if m else "sparse" for m in modes]
+                assert any("Mask Sparsity" in l for l in log.lines)
+            modes = [O.MODE_BLOCK_DIAGONAL if m == "block_diagonal" else O.MODE_SPARSE
+                     for m in st["mode"]]
+            sel = O.choose_topk_lines(xc, xl, n, T, top_k)
+            mask_ref = O.generate_mask_from_lines(sel, modes, seq_len=N, block_size=bs,
+                                                  video_tokens=N, text_tokens=0, bpf=bpf,
+                                                  model_type="wan")
+            assert np.array_equal(st["mask"].cpu().numpy(), mask_ref)
+            history_x.append(xc)
+        if phase == "sparse":
+            mask = st["mask"].cpu().numpy()
+            counts, lists = O.tiles_from_mask(mask, bs, tile_rows == "union")
+            tm = O.token_mask_from_tiles(lists, H, N, N)
+            ref, _ = O.masked_attention(qn, kn, vn, tm, dtype=np.float64)
+            _check_attn(out[0], ref, f"sparse step {step}", sparse=True)
+            assert info["mask"] is st["mask"]
+    assert len(history_x) == 3  # predict at W-1 and refreshes at W+T-1, W+2T-1
+
+
+def test_use_dense_and_error_paths():
+    H, S, D = 1, 256, 64
+    q, k, v = (torch.randn(1, H, S, D).to(torch.bfloat16).to(DEV) for _ in range(3))
+    st = md.create_adaptive_mask_state("wan", H, S, 0, 128, 2, warmup_steps=6, block_size=64)
+    out, info = md.SparseAttentionWithMap(q, k, v, st, None, current_step=0, use_dense=True)
+    ref, _ = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), None, dtype=np.float64)
+    _check_attn(out[0], ref, "use_dense")
+    with pytest.raises(RuntimeError, match="use_dense"):
+        md.SparseAttentionWithMap(q, k, v, st, None, current_step=0)
+    with pytest.raises(RuntimeError, match="no mask"):
+        md.SparseAttentionWithMap(q, k, v, st, None, current_step=7)
+    st2 = md.create_adaptive_mask_state("wan", H, S, 0, 128, 2, sparse_type="radial")
+    with pytest.raises(NotImplementedError):
+        md.SparseAttentionWithMap(q, k, v, st2, None, current_step=20)
