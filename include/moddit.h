@@ -166,13 +166,17 @@ int moddit_mask_from_lines(const int32_t* sel, int heads, int k, const uint8_t* 
                            moddit_stream_t stream);
 
 /*
- * Tile lists from an explicit bool block mask (H,nb,nb) at block_size granularity, the
- * same encoding as moddit_mask_from_lines; key tiles at or beyond kv_tiles are dropped.
+ * Tile lists from an explicit bool block mask at block_size granularity, the same
+ * encoding as moddit_mask_from_lines. The mask has n_rows query blocks and n_cols key
+ * blocks per head and is addressed as mask[h*mask_head_stride + i*mask_row_stride + j]
+ * (views such as the video rows of a larger mask need no copy); key tiles at or beyond
+ * kv_tiles are dropped. n_qtiles = ceil(n_rows*block_size/128), cap >= n_cols*block_size/64.
  * Replaces the mask conversion of AttentionSparseEngine (MoD/mod/attn_mask.py:296-311).
  */
-int moddit_mask_to_tiles(const uint8_t* mask, int heads, int nb, int block_size, int union_rows,
-                         int kv_tiles, int32_t* counts, int32_t* entries, int n_qtiles, int cap,
-                         moddit_stream_t stream);
+int moddit_mask_to_tiles(const uint8_t* mask, int heads, int n_rows, int n_cols,
+                         int64_t mask_head_stride, int64_t mask_row_stride, int block_size,
+                         int union_rows, int kv_tiles, int32_t* counts, int32_t* entries,
+                         int n_qtiles, int cap, moddit_stream_t stream);
 
 /*
  * Refresh merge: out[h,i,j] = mask[h,i,j] ? cur[h,i,j] : prev[h,i,j] over (H,n,n) fp16,

@@ -43,7 +43,8 @@ _SIGNATURES = {
     "moddit_check_bd": (_i, [_vp, _i, _i, _f, _vp, _vp]),
     "moddit_mask_from_lines": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _i, _i, _i, _i,
                                     _vp, _vp, _vp, _i, _i, _vp]),
-    "moddit_mask_to_tiles": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp]),
+    "moddit_mask_to_tiles": (_i, [_vp, _i, _i, _i, ctypes.c_int64, ctypes.c_int64, _i, _i, _i,
+                                  _vp, _vp, _i, _i, _vp]),
     "moddit_refresh_merge": (_i, [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, _i, _i,
                                   _vp, _vp]),
 }

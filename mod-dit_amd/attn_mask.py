@@ -224,22 +224,42 @@ def _log_sparsity(logger, layer_idx: int, mask: torch.Tensor) -> None:
         logger.info(f"Layer {layer_idx}, Mask Sparsity: {1 - mask.float().mean():.3%}")
 
 
-def _kv_border(pre_defined_mask: torch.Tensor) -> int:
+def _kv_valid(pre_defined_mask: torch.Tensor) -> int:
+    """Number of valid keys: the first row of the processor's padding mask.
+
+    Like the reference (MoD/mod/attn_mask.py:270,310), this reads one value on the host.
+    """
     return int(pre_defined_mask[0].sum().item())
 
 
 def _engine(query, key, value, mask, tiles, pre_defined_mask, video_token_num, block_size,
             union_rows):
-    if pre_defined_mask is not None:
-        raise NotImplementedError(
-            "AttentionSparseEngine: the text-token tail with pre_defined_mask (Hunyuan layout) "
-            "is not implemented in this build"
-        )
     if mask.dim() == 2:
         mask = mask.unsqueeze(0).expand(query.shape[1], -1, -1)
-    if tiles is None:
-        tiles = ops.mask_to_tiles(mask, block_size, union_rows=union_rows)
-    out, _ = ops.block_sparse_fwd(query, key, value, tiles)
+    if pre_defined_mask is None:
+        if tiles is None:
+            tiles = ops.mask_to_tiles(mask, block_size, union_rows=union_rows)
+        out, _ = ops.block_sparse_fwd(query, key, value, tiles)
+        return out
+    # Hunyuan layout (MoD/mod/attn_mask.py:310-331): video queries run block-sparse over the
+    # key tiles below ceil(valid/64) (so up to 63 padded text keys of the last tile take
+    # part, as in the reference); text queries attend densely to the valid keys.
+    S = query.shape[2]
+    kv = _kv_valid(pre_defined_mask)
+    kv_tiles = (kv + 63) // 64
+    video = int(video_token_num)
+    if video % block_size:
+        raise ValueError(f"video_token_num={video} must be divisible by block_size={block_size}")
+    out = torch.empty_like(query, memory_format=torch.contiguous_format)
+    if video > 0:
+        vt = ops.mask_to_tiles(mask[:, :video // block_size, :], block_size, union_rows=union_rows,
+                               kv_tiles=kv_tiles)
+        kv_len = min(S, kv_tiles * 64)
+        ops.block_sparse_fwd(query[:, :, :video], key[:, :, :kv_len], value[:, :, :kv_len], vt,
+                             out=out[:, :, :video])
+    if video < S:
+        ops.flash_fwd(query[:, :, video:], key[:, :, :kv], value[:, :, :kv], return_lse=False,
+                      out=out[:, :, video:])
     return out
 
 
@@ -255,10 +275,11 @@ def AttentionSparseEngine(query, key, value, mask, pre_defined_mask=None, video_
 
 
 def _dense_engine(query, key, value, pre_defined_mask):
+    """All-True mask: every query attends to the valid keys (MoD/mod/attn_mask.py:268-295;
+    the reference's video/text split there is the same computation)."""
     if pre_defined_mask is not None:
-        raise NotImplementedError(
-            "dense engine with pre_defined_mask (Hunyuan text tail) is not implemented in this build"
-        )
+        kv = _kv_valid(pre_defined_mask)
+        key, value = key[:, :, :kv], value[:, :, :kv]
     out, _ = ops.flash_fwd(query, key, value, return_lse=False)
     return out
 

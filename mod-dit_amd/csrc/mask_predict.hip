@@ -422,7 +422,10 @@ struct MaskParams {
   int text_blocks;
   int block;               // 64 or 128
   int union_rows;
-  const uint8_t* mask_in;  // (H, nb, nb) when from_mask
+  const uint8_t* mask_in;  // (H, n_rows, nb) addressed with the strides below (from_mask)
+  int64_t in_head_stride;
+  int64_t in_row_stride;
+  int n_rows;              // mask rows (query blocks); == nb when built from lines
   uint8_t* mask_out;       // (H, nb, nb) or null
   int32_t* counts;         // (H, n_qtiles) or null
   int32_t* entries;        // (H, n_qtiles, cap) or null
@@ -470,10 +473,11 @@ __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) 
   const int rows_per_tile = p.block == 64 ? 2 : 1;
   const int r0 = t * rows_per_tile;
   const int r1 = r0 + 1;
-  const bool has_r1 = rows_per_tile == 2 && r1 < nb;
+  const int n_rows = p.n_rows;
+  const bool has_r1 = rows_per_tile == 2 && r1 < n_rows;
 
   auto cell = [&](int i, int j) -> bool {
-    if (kFromMask) return p.mask_in[(static_cast<int64_t>(h) * nb + i) * nb + j] != 0;
+    if (kFromMask) return p.mask_in[h * p.in_head_stride + i * p.in_row_stride + j] != 0;
     switch (p.layout) {
       case MODDIT_LAYOUT_WAN:
         return video_cell(colsel, diagsel, mode, n, p.bpf, i, j);
@@ -498,10 +502,10 @@ __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) 
   // pass 1: mask bytes + entry count
   int cnt = 0;
   for (int j = j0; j < j1; ++j) {
-    const bool m0 = r0 < nb && cell(r0, j);
+    const bool m0 = r0 < n_rows && cell(r0, j);
     const bool m1 = has_r1 && cell(r1, j);
     if (!kFromMask && p.mask_out) {
-      if (r0 < nb) p.mask_out[(static_cast<int64_t>(h) * nb + r0) * nb + j] = m0;
+      if (r0 < n_rows) p.mask_out[(static_cast<int64_t>(h) * nb + r0) * nb + j] = m0;
       if (has_r1) p.mask_out[(static_cast<int64_t>(h) * nb + r1) * nb + j] = m1;
     }
     if (m0 || m1) {
@@ -537,7 +541,7 @@ __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) 
   const int64_t slot = static_cast<int64_t>(h) * p.n_qtiles + t;
   int32_t* out = p.entries + slot * p.cap;
   for (int j = j0; j < j1; ++j) {
-    const bool m0 = r0 < nb && cell(r0, j);
+    const bool m0 = r0 < n_rows && cell(r0, j);
     const bool m1 = has_r1 && cell(r1, j);
     if (!(m0 || m1)) continue;
     int bits;
@@ -698,8 +702,8 @@ extern "C" int moddit_check_bd(const float* x, int heads, int features, float th
   return MODDIT_OK;
 }
 
-static int check_tile_outputs(int nb, int block_size, int n_qtiles, int cap) {
-  const int64_t tokens = static_cast<int64_t>(nb) * block_size;
+static int check_tile_outputs(int n_rows, int nb, int block_size, int n_qtiles, int cap) {
+  const int64_t tokens = static_cast<int64_t>(n_rows) * block_size;
   const int64_t need_q = (tokens + 127) / 128;
   MODDIT_CHECK_ARG(n_qtiles == need_q, "mask tiles: n_qtiles=%d but %lld mask tokens need %lld",
                    n_qtiles, static_cast<long long>(tokens), static_cast<long long>(need_q));
@@ -727,7 +731,7 @@ extern "C" int moddit_mask_from_lines(const int32_t* sel, int heads, int k, cons
     MODDIT_CHECK_ARG(text_blocks >= 0 && nb - text_blocks == n,
                      "mask_from_lines: cogvideox layout needs nb - text_blocks == n");
   if (counts) {
-    int rc = check_tile_outputs(nb, block_size, n_qtiles, cap);
+    int rc = check_tile_outputs(nb, nb, block_size, n_qtiles, cap);
     if (rc) return rc;
   } else {
     n_qtiles = static_cast<int>((static_cast<int64_t>(nb) * block_size + 127) / 128);
@@ -745,6 +749,7 @@ extern "C" int moddit_mask_from_lines(const int32_t* sel, int heads, int k, cons
   p.block = block_size;
   p.union_rows = union_rows;
   p.mask_out = mask_out;
+  p.n_rows = nb;
   p.counts = counts;
   p.entries = entries;
   p.n_qtiles = n_qtiles;
@@ -759,24 +764,30 @@ extern "C" int moddit_mask_from_lines(const int32_t* sel, int heads, int k, cons
   return MODDIT_OK;
 }
 
-extern "C" int moddit_mask_to_tiles(const uint8_t* mask, int heads, int nb, int block_size,
-                                    int union_rows, int kv_tiles, int32_t* counts,
-                                    int32_t* entries, int n_qtiles, int cap,
+extern "C" int moddit_mask_to_tiles(const uint8_t* mask, int heads, int n_rows, int n_cols,
+                                    int64_t mask_head_stride, int64_t mask_row_stride,
+                                    int block_size, int union_rows, int kv_tiles,
+                                    int32_t* counts, int32_t* entries, int n_qtiles, int cap,
                                     moddit_stream_t stream) {
   clear_error();
   MODDIT_CHECK_ARG(mask && counts && entries, "mask_to_tiles: null pointer argument");
-  MODDIT_CHECK_ARG(heads >= 0 && nb > 0, "mask_to_tiles: invalid shape");
+  MODDIT_CHECK_ARG(heads >= 0 && n_rows > 0 && n_cols > 0, "mask_to_tiles: invalid shape");
+  MODDIT_CHECK_ARG(mask_head_stride >= 0 && mask_row_stride >= n_cols,
+                   "mask_to_tiles: invalid mask strides");
   MODDIT_CHECK_ARG(block_size == 64 || block_size == 128, "mask_to_tiles: block_size must be 64 or 128");
-  int rc = check_tile_outputs(nb, block_size, n_qtiles, cap);
+  int rc = check_tile_outputs(n_rows, n_cols, block_size, n_qtiles, cap);
   if (rc) return rc;
   if (heads == 0) return MODDIT_OK;
   MaskParams p{};
   p.n = 1;
   p.bpf = 1;
-  p.nb = nb;
+  p.nb = n_cols;
+  p.n_rows = n_rows;
   p.block = block_size;
   p.union_rows = union_rows;
   p.mask_in = mask;
+  p.in_head_stride = mask_head_stride;
+  p.in_row_stride = mask_row_stride;
   p.counts = counts;
   p.entries = entries;
   p.n_qtiles = n_qtiles;

@@ -256,24 +256,27 @@ def mask_from_lines(sel, mode, *, n, blocks_per_frame, layout, nb, text_blocks, 
 
 
 def mask_to_tiles(mask: torch.Tensor, block_size: int, union_rows=True, kv_tiles=None) -> TileList:
-    """TileList of an explicit bool (H,nb,nb) block mask."""
+    """TileList of a bool (H, rows, cols) block mask (strided views are read in place)."""
     _require_gpu(mask, what="mask_to_tiles")
-    if mask.ndim != 3 or mask.shape[1] != mask.shape[2]:
-        raise ValueError(f"mask must be (H, nb, nb), got {tuple(mask.shape)}")
+    if mask.ndim != 3:
+        raise ValueError(f"mask must be (H, rows, cols), got {tuple(mask.shape)}")
     if mask.dtype != torch.bool:
         mask = mask != 0
-    mask = mask.contiguous()
-    H, nb, _ = mask.shape
-    nq, cap = _tile_shape(nb, block_size)
+    if mask.stride(2) != 1 or mask.stride(1) < mask.shape[2]:
+        mask = mask.contiguous()
+    H, rows, cols = mask.shape
+    nq = (rows * block_size + 127) // 128
+    cap = cols * (block_size // 64)
     if kv_tiles is None:
         kv_tiles = cap
     tiles = TileList(torch.empty((H, nq), device=mask.device, dtype=torch.int32),
                      torch.empty((H, nq, cap), device=mask.device, dtype=torch.int32),
                      block_size, bool(union_rows))
-    check(_lib.load().moddit_mask_to_tiles(mask.data_ptr(), H, nb, int(block_size),
-                                           int(bool(union_rows)), int(kv_tiles),
-                                           tiles.counts.data_ptr(), tiles.entries.data_ptr(), nq,
-                                           cap, _stream(mask)), "moddit_mask_to_tiles")
+    check(_lib.load().moddit_mask_to_tiles(mask.data_ptr(), H, rows, cols, mask.stride(0),
+                                           mask.stride(1), int(block_size), int(bool(union_rows)),
+                                           int(kv_tiles), tiles.counts.data_ptr(),
+                                           tiles.entries.data_ptr(), nq, cap, _stream(mask)),
+          "moddit_mask_to_tiles")
     return tiles
 
 

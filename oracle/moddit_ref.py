@@ -319,11 +319,14 @@ def mask_cell(sel_h: Sequence[int], mode: int, n: int, bpf: int, i: int, j: int)
 # --------------------------------------------------------------------------------------
 def tiles_from_mask(mask: np.ndarray, block_size: int, union_rows: bool,
                     kv_tiles: Optional[int] = None) -> Tuple[np.ndarray, List[List[List[int]]]]:
-    """Per (head, 128-row query tile) ascending entries (key_tile << 2 | row bits)."""
-    H, nb, _ = mask.shape
-    nq = (nb * block_size + 127) // 128
+    """Per (head, 128-row query tile) ascending entries (key_tile << 2 | row bits).
+
+    mask: bool (H, rows, cols) block mask (rows = query blocks, cols = key blocks).
+    """
+    H, rows, cols = mask.shape
+    nq = (rows * block_size + 127) // 128
     per_col = block_size // 64
-    cap = nb * per_col
+    cap = cols * per_col
     if kv_tiles is None:
         kv_tiles = cap
     counts = np.zeros((H, nq), dtype=np.int32)
@@ -334,15 +337,15 @@ def tiles_from_mask(mask: np.ndarray, block_size: int, union_rows: bool,
             ent = []
             if block_size == 64:
                 r0, r1 = 2 * t, 2 * t + 1
-                for j in range(nb):
-                    m0 = bool(mask[h, r0, j]) if r0 < nb else False
-                    m1 = bool(mask[h, r1, j]) if r1 < nb else False
+                for j in range(cols):
+                    m0 = bool(mask[h, r0, j]) if r0 < rows else False
+                    m1 = bool(mask[h, r1, j]) if r1 < rows else False
                     if m0 or m1:
                         bits = 3 if union_rows else (int(m0) | (int(m1) << 1))
                         if j < kv_tiles:
                             ent.append((j << 2) | bits)
             else:
-                for j in range(nb):
+                for j in range(cols):
                     if mask[h, t, j]:
                         for s in range(2):
                             if 2 * j + s < kv_tiles:

@@ -134,6 +134,53 @@ def test_schedule_matches_oracle_stage_by_stage(tile_rows):
     assert len(history_x) == 3  # predict at W-1 and refreshes at W+T-1, W+2T-1
 
 
+@pytest.mark.parametrize("tile_rows", ["exact", "union"])
+@pytest.mark.parametrize("bs", [64, 128])
+def test_hunyuan_text_tail_with_padding_mask(tile_rows, bs):
+    """Hunyuan layout: video first, then text of which only `valid_text` tokens are real.
+
+    Dense steps attend to the valid keys; sparse steps run video queries block-sparse over
+    the key tiles below ceil(valid/64) (MoD/mod/attn_mask.py:310-317) and text queries
+    densely over the valid keys (:319-330).
+    """
+    H, F, tpf, D = 2, 3, 512, 64
+    video, text, valid_text = F * tpf, 256, 150
+    S = video + text
+    W, T, top_k, thr = 4, 3, 30, 1e-3
+    st = md.create_adaptive_mask_state("hunyuan", H, video, text, tpf, F, warmup_steps=W,
+                                       top_k=top_k, predict_T=T, threshold=thr, block_size=bs,
+                                       tile_rows=tile_rows)
+    valid = video + valid_text
+    pdm = torch.zeros(S, S, dtype=torch.bool, device=DEV)
+    pdm[:, :valid] = True
+    for step in range(W + T):
+        q, k, v = _structured_qkv(H, 1, S, D, seed=100 + step)
+        qn, kn, vn = (_np(t[0]) for t in (q, k, v))
+        phase = O.step_phase(step, W, T)
+        out, _ = md.SparseAttentionWithMap(q, k, v, st, None, pre_defined_mask=pdm,
+                                           current_step=step, use_dense=step < W - 2)
+        if phase == "dense":
+            tm = np.zeros((H, S, S), bool)
+            tm[:, :, :valid] = True
+            ref, _ = O.masked_attention(qn, kn, vn, tm, dtype=np.float64)
+            _check_attn(out[0], ref, f"hunyuan dense {step}")
+        elif phase == "sparse":
+            mask = st["mask"].cpu().numpy()
+            nbv = video // bs
+            assert mask.shape == (H, S // bs, S // bs) and mask[:, nbv:, :].all() and mask[:, :, nbv:].all()
+            kv_tiles = (valid + 63) // 64
+            _, lists = O.tiles_from_mask(mask[:, :nbv, :], bs, tile_rows == "union", kv_tiles=kv_tiles)
+            tm = np.zeros((H, S, S), bool)
+            tm[:, :video, :] = O.token_mask_from_tiles(lists, H, video, S)
+            tm[:, video:, :valid] = True
+            ref, _ = O.masked_attention(qn, kn, vn, tm, dtype=np.float64)
+            _check_attn(out[0], ref, f"hunyuan sparse {step}", sparse=True)
+        else:
+            # map steps: dense pass without the padding mask (MoD/mod/attn_mask.py:633)
+            ref, _ = O.masked_attention(qn, kn, vn, None, dtype=np.float64)
+            _check_attn(out[0], ref, f"hunyuan map step {step}")
+
+
 def test_use_dense_and_error_paths():
     H, S, D = 1, 256, 64
     q, k, v = (torch.randn(1, H, S, D).to(torch.bfloat16).to(DEV) for _ in range(3))
