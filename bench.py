@@ -171,6 +171,121 @@ def time_events(fn, reps):
 
 
 # ------------------------------------------------------------------------------------
+# denoising-trajectory sweep
+# ------------------------------------------------------------------------------------
+def _phase(step, W, T):
+    """Schedule of MoD/mod/attn_mask.py:598-712 with the processors' use_dense gate."""
+    if step < W - 2:
+        return "dense"
+    if step < W:
+        return "map_fit" if step == W - 2 else "map_fit_predict"
+    return "refresh" if (step - W) % T == T - 1 else "sparse"
+
+
+def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps=50, W=12, T=10):
+    """50 steps on one layer: dense warmup, map+fit steps, then sparse steps that each re-run
+    the fit, line selection and mask/tiles before the sparse attention, with refreshes
+    (dense + map + merge + fit) every T steps. The target sparsity ramps linearly from 50 %
+    to 90 % through top_k (one per step, bisected beforehand on the predicted features);
+    per-head sparsity varies with each head's own predicted lines."""
+    n = art["n"]
+    modes = art["modes"]
+    x_cur, x_last, smap = art["x_cur"], art["x_last"], art["smap"]
+    ginv = md.lstsq.get_inverse(q.device, n, bpf, 1.0)
+
+    def build(top_k, xc, xl):
+        sel = ops.select_lines(xc, xl, n, T, top_k)
+        return ops.mask_from_lines(sel, modes, n=n, blocks_per_frame=bpf, layout=md._lib.LAYOUT_WAN,
+                                   nb=n, text_blocks=0, block_size=bs, union_rows=union)
+
+    targets = [0.5 + 0.4 * s / (steps - 1) for s in range(steps)]
+    topk_for = {}
+    for tgt in sorted(set(round(t, 3) for t in targets)):
+        lo, hi, best = 1, 3 * n - 1, None
+        while lo <= hi:
+            mid = (lo + hi) // 2
+            m, _ = build(mid, x_cur, x_last)
+            sp = 1.0 - m.float().mean().item()
+            if best is None or abs(sp - tgt) < abs(best[1] - tgt):
+                best = (mid, sp)
+            if sp > tgt:
+                lo = mid + 1
+            else:
+                hi = mid - 1
+        topk_for[tgt] = best[0]
+
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+    rows = []
+    mask, tiles = build(topk_for[round(targets[0], 3)], x_cur, x_last)
+    torch.cuda.synchronize()
+    t_all0 = time.perf_counter()
+    for s in range(steps):
+        ph = _phase(s, W, T)
+        top_k = topk_for[round(targets[s], 3)]
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record(stream)
+        if ph == "dense":
+            ops.flash_fwd(q, k, v, return_lse=False, out=out)
+            e[1].record(stream)
+            e[2].record(stream)
+        elif ph in ("map_fit", "map_fit_predict", "refresh"):
+            _, cur_map = md.flash_attn_with_sparsity_map(q, k, v, threshold, bs, model_type="wan")
+            cur_map = cur_map[0]
+            if ph == "refresh":
+                cur_map = ops.refresh_merge(smap, cur_map, mask)
+            e[1].record(stream)
+            if ph != "map_fit":
+                x_new = ops.solve(ginv, ops.compute_mts(cur_map, bpf))
+                x_last, x_cur = x_cur, x_new
+                mask, tiles = build(top_k, x_cur, x_last)
+            smap = cur_map
+            e[2].record(stream)
+        else:
+            e[1].record(stream)
+            x_new = ops.solve(ginv, ops.compute_mts(smap, bpf))
+            mask, tiles = build(top_k, x_new, x_last)
+            e[2].record(stream)
+            ops.block_sparse_fwd(q, k, v, tiles, out=out)
+        e3 = torch.cuda.Event(enable_timing=True)
+        e3.record(stream)
+        e3.synchronize()
+        first = e[0].elapsed_time(e[1])
+        over = e[1].elapsed_time(e[2])
+        attn = e[2].elapsed_time(e3)
+        sp = 1.0 - mask.float().mean().item() if ph in ("sparse", "refresh", "map_fit_predict") else 0.0
+        if ph == "sparse":
+            rows.append(dict(step=s, phase=ph, ms=round(over + attn, 3), attn_ms=round(attn, 3),
+                             overhead_ms=round(over, 4), sparsity=round(sp, 4), top_k=top_k))
+        else:
+            rows.append(dict(step=s, phase=ph, ms=round(first + over + attn, 3),
+                             attn_ms=round(first, 3), overhead_ms=round(over, 4),
+                             sparsity=round(sp, 4), top_k=top_k))
+    torch.cuda.synchronize()
+    total_ms = (time.perf_counter() - t_all0) * 1e3
+    dense_ms = sorted(r["attn_ms"] for r in rows if r["phase"] == "dense")[len([r for r in rows if r["phase"] == "dense"]) // 2]
+    sparse_rows = [r for r in rows if r["phase"] == "sparse"]
+    mean_sparse = sum(r["ms"] for r in sparse_rows) / len(sparse_rows)
+    mean_over = sum(r["overhead_ms"] for r in sparse_rows) / len(sparse_rows)
+    return {
+        "metric": "configs[4] denoising-trajectory sweep: per-step latency and mask-overhead fraction",
+        "config": {"workload": f"{config}-like layer, 50 steps, W={W}, T={T}, sparsity 50%->90%",
+                   "H": H, "N": N, "d": D, "block": bs, "tile_rows": "union" if union else "exact"},
+        "dense_ms": round(dense_ms, 3),
+        "mean_sparse_step_ms": round(mean_sparse, 3),
+        "mean_sparse_overhead_ms": round(mean_over, 4),
+        "mean_overhead_frac_of_dense": round(mean_over / dense_ms, 5),
+        "trajectory_ms": round(sum(r["ms"] for r in rows), 2),
+        "trajectory_wall_ms": round(total_ms, 2),
+        "all_dense_trajectory_ms": round(dense_ms * steps, 2),
+        "trajectory_speedup_vs_dense": round(dense_ms * steps / sum(r["ms"] for r in rows), 3),
+        "steps": rows,
+        "dtype": "bf16",
+        "data": "synthetic (seeded structured Q/K/V, same inputs every step)",
+    }
+
+
+# ------------------------------------------------------------------------------------
 # CPU baseline (the oracle's block-sparse attention on a bounded sample)
 # ------------------------------------------------------------------------------------
 def cpu_baseline(q, k, v, tiles, budget_s=12.0):
@@ -232,6 +347,9 @@ def main(argv=None):
     ap.add_argument("--threshold", type=float, default=1e-4)
     ap.add_argument("--dense-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweep", action="store_true",
+                    help="configs[4]: 50-step denoising trajectory (W=12, T=10) with sparsity "
+                         "ramping 50%%->90%%; prints its own JSON line")
     ap.add_argument("--profile", choices=("sparse", "dense", "replay", "mask", "copy"), default=None,
                     help="run only the named kernel(s) after setup (for rocprofv3 counter passes); "
                          "prints no JSON")
@@ -283,6 +401,12 @@ def main(argv=None):
 
     def sparse_call():
         ops.block_sparse_fwd(q, k, v, tiles, out=out)
+
+    if args.sweep:
+        result = run_sweep(q, k, v, art, H=H, N=N, D=D, bpf=bpf, bs=bs, union=union,
+                           threshold=args.threshold, config=args.config)
+        print(json.dumps(result), flush=True)
+        return 0
 
     if args.profile is not None:
         for _ in range(args.steps):
