@@ -9,13 +9,16 @@
 // the rescale of O is a per-lane multiply. The S^T accumulator layout is exactly the
 // B-operand layout P^T needs, so P never leaves registers.
 //
-// LDS per stage: K row-major [64][d] (pitch 2d+16 B) and V transposed [d][64]
-// (pitch 136 B); two stages double-buffer the tiles, filled from registers that were
-// loaded from global memory during the previous tile's math.
+// K and V tiles go straight from HBM into LDS (buffer_load ... lds, no register
+// staging), both row-major with an XOR swizzle on 16-byte chunks that keeps the operand
+// reads bank-conflict free; V^T fragments come out of the row-major V tile through
+// ds_read_b64_tr_b16. Two stages per operand. The loop is software pipelined:
+// iteration j computes S_{j+1} and O += P_j V_j while K_{j+2} and V_{j+1} stream in, then
+// the softmax of S_{j+1}; one barrier per tile.
 //
 // The sparse variant walks a per-(head, query tile) list of key tiles, each entry
 // carrying two row bits (query rows 0-63 / 64-127 of the tile); a wave whose bit is
-// clear skips the math but still helps stage the tile.
+// clear skips the math but still issues its share of the tile's DMA.
 //
 // Reference semantics: flash_attn_func (MoD/mod/triton_flash_sparsity.py:320-321) for
 // the dense pass incl. its LSE; block_sparse_sage2_attn_cuda at 128q x 64k tiles
@@ -32,12 +35,13 @@ constexpr int kThreads = 256;
 
 template <int D>
 struct AttnLds {
-  static constexpr int kPitchK = D * 2 + 16;  // bytes per K row (68 dwords for d=128: 4 mod 64 banks)
-  static constexpr int kPitchV = kBN * 2 + 16;  // bytes per V^T row (36 dwords: 16 lanes hit 16 bank quads)
-  static constexpr int kKBytes = kBN * kPitchK;
-  static constexpr int kVBytes = D * kPitchV;
-  static constexpr int kStage = kKBytes + kVBytes;
-  static constexpr int kTotal = 2 * kStage;
+  static constexpr int kRowBytes = D * 2;                 // one token row, no padding
+  static constexpr int kTileBytes = kBN * kRowBytes;      // one 64-key K or V tile
+  static constexpr int kTotal = 4 * kTileBytes;           // K ring (2) + V ring (2)
+  static constexpr int kChunks = D / 8;                   // 16-byte chunks per row
+  static constexpr int kRowsPerBankCycle = 128 / D;       // rows covering the 64 banks
+  static constexpr int kRowsPerWindow = 1024 / kRowBytes; // rows per 1 KB DMA window
+  static constexpr int kWindows = kTileBytes / 1024;      // DMA windows per tile
 };
 
 struct AttnParams {
@@ -63,30 +67,68 @@ struct AttnParams {
   uint32_t v_bytes;
 };
 
-// Rows of a 64-key tile are stored in LDS in the order pi(r): inside every 16-row chunk
-// the row groups [4,8) and [8,12) are swapped. With that order the S^T accumulator of
-// lane half h holds keys 8h..8h+7 of each 16-key chunk, in order, so the matching V^T
-// operand is one 16-byte LDS read.
+// K rows are stored in LDS in the order pi(r): inside every 16-row chunk the row groups
+// [4,8) and [8,12) are swapped, so the S^T accumulator of lane half h holds keys
+// 8h..8h+7 of each 16-key chunk, in order (the P^T operand needs no shuffle).
 __device__ __forceinline__ int key_perm(int r) { return r ^ ((((r >> 2) ^ (r >> 3)) & 1) * 12); }
+
+// 16-byte chunk swizzles (XOR on the chunk index) that make the MFMA operand reads
+// bank-conflict free: K rows are read one row per lane (A operand of S^T), V rows
+// through ds_read_b64_tr_b16 (four keys x 32 dims per half-wave).
+template <int D>
+__device__ __forceinline__ int swz_k(int r) { return (r / (128 / D)) % (D / 8); }
+template <int D>
+__device__ __forceinline__ int swz_v(int key) { return 4 * ((key / (128 / D)) % (D / 32)); }
 
 // The running row max is only moved when a tile's max exceeds it by more than this many
 // log2 units; probabilities then stay <= 2^8 and the O rescale is skipped for whole
 // waves on most tiles. Softmax is shift-invariant, so results do not depend on it.
 constexpr float kRescaleSlack = 8.0f;
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// buffer_load_dwordx4 ... lds: lane l writes its 16 bytes at LDS byte m0 + 16*l. Issued as
+// inline asm so the compiler does not track it: it would otherwise wait for every
+// outstanding DMA before each LDS read it cannot disambiguate. Completion is established
+// explicitly (s_waitcnt vmcnt(0) + barrier) before any wave reads the written stage;
+// vmcnt waits the compiler emits for its own loads stay correct because vector loads
+// retire in issue order.
+__device__ __forceinline__ void lds_dma16(u32x4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds)
+               : "memory");
+}
+
+// Raw buffer descriptor: base, stride 0, num_records = bytes (range checked per lane).
+__device__ __forceinline__ u32x4 raw_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu, bytes,
+               0x00020000u};
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const unsigned char*)(p)));
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of the
+// 4-element rows addressed by lanes i/4, i/4+4, i/4+8, i/4+12.
+__device__ __forceinline__ s16x4 lds_read_tr16(const unsigned char* a) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(a));
+}
+
 template <int D, typename E, bool kSparse, bool kRagged>
-__global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p) {
+__global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fwd_kernel(AttnParams p) {
   using L = AttnLds<D>;
   using V8 = typename E::vec8;
-  constexpr int kDChunks = D / 16;                       // MFMA k-steps over d for S^T
-  constexpr int kDSub = D / 32;                          // 32-row blocks of O^T
-  constexpr int kVecPerRow = D / 8;                      // 16-byte vectors per token row
-  constexpr int kKVecs = kBN * kVecPerRow / kThreads;    // K vectors per thread
-  constexpr int kKRowStep = kThreads / kVecPerRow;       // K rows between a thread's vectors
-  constexpr int kKeysPerThr = D / 32;                    // V keys per thread (x 8 dims)
-  constexpr int kKeyGroups = kBN / kKeysPerThr;          // V key groups per tile
+  constexpr int kDChunks = D / 16;  // MFMA k-steps over d for S^T
+  constexpr int kDSub = D / 32;     // 32-row blocks of O^T
+  constexpr int kWinPerWave = L::kWindows / 4;
 
   extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* const k_ring = smem;
+  unsigned char* const v_ring = smem + 2 * L::kTileBytes;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -104,7 +146,6 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
   const uint16_t* kb = p.k + b * p.k_sb + h * p.k_sh;
   const uint16_t* vb = p.v + b * p.v_sb + h * p.v_sh;
 
-  // ---- tile list ----
   int n_iter;
   const int32_t* list = nullptr;
   if (kSparse) {
@@ -125,77 +166,71 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
     const u32x4* src = reinterpret_cast<const u32x4*>(qb + r * p.q_ss);
 #pragma unroll
     for (int c = 0; c < kDChunks; ++c) qf[c] = as_vec8<V8>(src[2 * c + half]);
-    // Sparse: retire the Q loads here, otherwise the waitcnt pass keeps them pending
-    // across the loop back-edge and every tile's first MFMAs wait for the K/V prefetch.
-    // Dense: measured faster without it (the in-order wait de-phases the two waves that
-    // share a SIMD), so it is left to the compiler there.
-    if constexpr (kSparse) __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_waitcnt(0);
   }
 
-  // ---- global -> register staging of one K/V tile ----
-  // K: thread owns column k_col of rows k_row0 + i*kKRowStep (row-major, 256 B rows).
-  // V: thread owns keys v_kgrp*kKeysPerThr + j, dims v_dgrp*8.. (transposed into LDS).
-  const int k_col = tid % kVecPerRow;
-  const int k_row0 = tid / kVecPerRow;
-  const int v_kgrp = tid % kKeyGroups;
-  const int v_dgrp = tid / kKeyGroups;
-  // Buffer resources over this head's K/V rows; the byte span was checked on the host.
-  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kb, p.k_bytes);
-  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vb, p.v_bytes);
-  const uint32_t k_voff = static_cast<uint32_t>((k_row0 * p.k_ss + k_col * 8) * 2);
-  const uint32_t v_voff = static_cast<uint32_t>((v_kgrp * kKeysPerThr * p.v_ss + v_dgrp * 8) * 2);
-  const uint32_t k_row_step = static_cast<uint32_t>(kKRowStep * p.k_ss * 2);
+  // ---- direct global -> LDS staging (buffer_load ... lds, 16 B per lane) ----
+  // DMA window w writes LDS bytes [w*1024, w*1024+1024) of a stage, lane l at l*16. The
+  // per-lane source is chosen so that the window holds the swizzled rows.
+  const u32x4 k_rsrc = raw_rsrc(kb, p.k_bytes);
+  const u32x4 v_rsrc = raw_rsrc(vb, p.v_bytes);
+  const uint32_t k_lds = lds_addr(k_ring);
+  const uint32_t v_lds = lds_addr(v_ring);
+  uint32_t k_src[kWinPerWave];
+  uint32_t v_src[kWinPerWave];
+#pragma unroll
+  for (int i = 0; i < kWinPerWave; ++i) {
+    const int w = wave * kWinPerWave + i;
+    const int r = w * L::kRowsPerWindow + (lane * 16) / L::kRowBytes;  // LDS row
+    const int pch = ((lane * 16) % L::kRowBytes) / 16;                  // physical chunk
+    const int kq = pch ^ swz_k<D>(r);                                   // logical chunk
+    const int vq = pch ^ swz_v<D>(r);
+    k_src[i] = static_cast<uint32_t>((key_perm(r) * p.k_ss + kq * 8) * 2);
+    v_src[i] = static_cast<uint32_t>((r * p.v_ss + vq * 8) * 2);
+  }
   const uint32_t k_tile_bytes = static_cast<uint32_t>(kBN * p.k_ss * 2);
-  const uint32_t v_row_bytes = static_cast<uint32_t>(p.v_ss * 2);
   const uint32_t v_tile_bytes = static_cast<uint32_t>(kBN * p.v_ss * 2);
-  u32x4 kreg[kKVecs];
-  u32x4 vreg[kKeysPerThr];
 
-  // Full tiles put the tile offset in the SGPR offset (loop-invariant VGPR offsets keep
-  // the loads free of register reuse hazards); the ragged variant puts it in the
-  // range-checked VGPR offset so rows past kv_len read as zeros.
-#define MODDIT_LOAD_TILE(KT)                                                              \
-  do {                                                                                    \
-    if constexpr (!kRagged) {                                                             \
-      const uint32_t kso_ = static_cast<uint32_t>(KT) * k_tile_bytes;                     \
-      const uint32_t vso_ = static_cast<uint32_t>(KT) * v_tile_bytes;                     \
-      _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_)                               \
-          kreg[i_] = buf_load16(k_rsrc, k_voff, kso_ + i_ * k_row_step);                  \
-      _Pragma("unroll") for (int j_ = 0; j_ < kKeysPerThr; ++j_)                          \
-          vreg[j_] = buf_load16(v_rsrc, v_voff, vso_ + j_ * v_row_bytes);                 \
-    } else {                                                                              \
-      const uint32_t kto_ = static_cast<uint32_t>(KT) * k_tile_bytes;                     \
-      const uint32_t vto_ = static_cast<uint32_t>(KT) * v_tile_bytes;                     \
-      _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_)                               \
-          kreg[i_] = buf_load16(k_rsrc, k_voff + kto_ + i_ * k_row_step, 0);              \
-      _Pragma("unroll") for (int j_ = 0; j_ < kKeysPerThr; ++j_)                          \
-          vreg[j_] = buf_load16(v_rsrc, v_voff + vto_ + j_ * v_row_bytes, 0);             \
-    }                                                                                     \
-  } while (0)
+  auto dma_k = [&](int kt, int stage) {
+    const uint32_t to = static_cast<uint32_t>(kt) * k_tile_bytes;
+#pragma unroll
+    for (int i = 0; i < kWinPerWave; ++i) {
+      const uint32_t dst = k_lds + stage * L::kTileBytes + (wave * kWinPerWave + i) * 1024;
+      if constexpr (kRagged)
+        lds_dma16(k_rsrc, dst, k_src[i] + to, 0);
+      else
+        lds_dma16(k_rsrc, dst, k_src[i], to);
+    }
+  };
+  auto dma_v = [&](int kt, int stage) {
+    const uint32_t to = static_cast<uint32_t>(kt) * v_tile_bytes;
+#pragma unroll
+    for (int i = 0; i < kWinPerWave; ++i) {
+      const uint32_t dst = v_lds + stage * L::kTileBytes + (wave * kWinPerWave + i) * 1024;
+      if constexpr (kRagged)
+        lds_dma16(v_rsrc, dst, v_src[i] + to, 0);
+      else
+        lds_dma16(v_rsrc, dst, v_src[i], to);
+    }
+  };
 
-#define MODDIT_STORE_TILE(STAGE)                                                          \
-  do {                                                                                    \
-    unsigned char* ks_ = smem + (STAGE) * L::kStage;                                      \
-    unsigned char* vs_ = ks_ + L::kKBytes;                                                \
-    _Pragma("unroll") for (int i_ = 0; i_ < kKVecs; ++i_) {                               \
-      const int row_ = key_perm(k_row0 + i_ * kKRowStep);                                 \
-      *reinterpret_cast<u32x4*>(ks_ + row_ * L::kPitchK + k_col * 16) = kreg[i_];         \
-    }                                                                                     \
-    _Pragma("unroll") for (int dd_ = 0; dd_ < 8; ++dd_) {                                 \
-      unsigned char* dst_ =                                                               \
-          vs_ + (v_dgrp * 8 + dd_) * L::kPitchV + v_kgrp * kKeysPerThr * 2;               \
-      const uint32_t sel_ = (dd_ & 1) ? 0x07060302u : 0x05040100u;                        \
-      if constexpr (kKeysPerThr == 4) {                                                   \
-        u32x2 w_;                                                                         \
-        w_.x = __builtin_amdgcn_perm(vreg[1][dd_ >> 1], vreg[0][dd_ >> 1], sel_);         \
-        w_.y = __builtin_amdgcn_perm(vreg[3][dd_ >> 1], vreg[2][dd_ >> 1], sel_);         \
-        *reinterpret_cast<u32x2*>(dst_) = w_;                                             \
-      } else {                                                                            \
-        *reinterpret_cast<uint32_t*>(dst_) =                                              \
-            __builtin_amdgcn_perm(vreg[1][dd_ >> 1], vreg[0][dd_ >> 1], sel_);            \
-      }                                                                                   \
-    }                                                                                     \
-  } while (0)
+  // ---- LDS operand addressing ----
+  // K (A operand of S^T): lane reads row c32 (+32), logical chunk 2c+half.
+  uint32_t k_rd[kDChunks];
+#pragma unroll
+  for (int c = 0; c < kDChunks; ++c)
+    k_rd[c] = static_cast<uint32_t>(c32 * L::kRowBytes + (((2 * c + half) ^ swz_k<D>(c32)) * 16));
+  // V (A operand of O^T, via ds_read_b64_tr_b16): in 16-lane group g (dgrp = g&1,
+  // hh = g>>1) lane t addresses key 8*hh + (t>>2) (+16c + 4s) and dims dsub*32 + 16*dgrp + 4*(t&3).
+  const int g16 = lane >> 4;
+  const int t16 = lane & 15;
+  const int v_key0 = 8 * (g16 >> 1) + (t16 >> 2);  // key within a 16-key chunk, s = 0
+  uint32_t v_rd[kDSub];
+#pragma unroll
+  for (int dsub = 0; dsub < kDSub; ++dsub) {
+    const int d = dsub * 32 + 16 * (g16 & 1) + 4 * (t16 & 3);
+    v_rd[dsub] = static_cast<uint32_t>(v_key0 * L::kRowBytes + (((d >> 3) ^ swz_v<D>(v_key0)) * 16) + (d & 7) * 2);
+  }
 
   f32x16 oacc[kDSub];
 #pragma unroll
@@ -203,118 +238,156 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
   float m_run = -INFINITY;
   float l_run = 0.f;
 
-  // Tile-list entries are uniform; decode with a clamp so a corrupt list can only select
-  // a wrong (in-bounds) tile, never address outside K/V.
   auto decode = [&](int e_raw, int& kt, int& flags) {
     const int e = __builtin_amdgcn_readfirstlane(e_raw);
     kt = e >> 2;
     kt = kt < 0 ? 0 : (kt < p.n_ktiles ? kt : p.n_ktiles - 1);
     flags = e & 3;
   };
-  auto entry = [&](int i) -> int {
-    return kSparse ? list[i] : ((i << 2) | 3);
+  auto entry = [&](int i) -> int { return kSparse ? list[i] : ((i << 2) | 3); };
+
+  auto qk = [&](const unsigned char* ks, f32x16& s0, f32x16& s1) {
+    s0 = f32x16{};
+    s1 = f32x16{};
+#pragma unroll
+    for (int c = 0; c < kDChunks; ++c) {
+      const V8 a0 = *reinterpret_cast<const V8*>(ks + k_rd[c]);
+      const V8 a1 = *reinterpret_cast<const V8*>(ks + k_rd[c] + 32 * L::kRowBytes);
+      s0 = E::mma(a0, qf[c], s0);
+      s1 = E::mma(a1, qf[c], s1);
+    }
+  };
+  auto pv = [&](const unsigned char* vs, const V8* pb) {
+#pragma unroll
+    for (int dsub = 0; dsub < kDSub; ++dsub) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const unsigned char* a = vs + v_rd[dsub] + c * 16 * L::kRowBytes;
+        const s16x4 lo = lds_read_tr16(a);
+        const s16x4 hi = lds_read_tr16(a + 4 * L::kRowBytes);
+        const u32x4 w = {__builtin_bit_cast(u32x2, lo).x, __builtin_bit_cast(u32x2, lo).y,
+                         __builtin_bit_cast(u32x2, hi).x, __builtin_bit_cast(u32x2, hi).y};
+        oacc[dsub] = E::mma(as_vec8<V8>(w), pb[c], oacc[dsub]);
+      }
+    }
+  };
+  auto softmax = [&](f32x16& s0, f32x16& s1, int kt, V8* pb, float& alpha, bool& rescale) {
+    if constexpr (kRagged) {
+      const int key0 = kt * kBN;
+      if (key0 + kBN > p.kv_len) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kr = (i >> 3) * 16 + 8 * half + (i & 7);
+          if (key0 + kr >= p.kv_len) s0[i] = -INFINITY;
+          if (key0 + 32 + kr >= p.kv_len) s1[i] = -INFINITY;
+        }
+      }
+    }
+    float mx = s0[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s0[i]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s1[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mxs = mx * p.scale_log2;
+    const bool need = mxs > m_run + kRescaleSlack;
+    rescale = __ballot(need) != 0ull;
+    const float m_new = need ? mxs : m_run;
+    // exp2(0) = 1 when the max is kept; fminf drops the NaN of -inf - -inf
+    alpha = __builtin_amdgcn_exp2f(__builtin_fminf(m_run - m_new, 0.f));
+    m_run = m_new;
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    float rs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], p.scale_log2, -m_use));
+      const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], p.scale_log2, -m_use));
+      rs += e0 + e1;
+      pb[i >> 3][i & 7] = static_cast<typename E::elem>(e0);
+      pb[2 + (i >> 3)][i & 7] = static_cast<typename E::elem>(e1);
+    }
+    l_run = l_run * alpha + rs;
   };
 
-  int e_cur = 0, e_next = 0;
+  // ---- prologue: K_0, V_0 -> stage 0, K_1 -> K stage 1; S_0 -> P_0 ----
+  V8 pb[4];
+  bool act_cur = false;
+  int e_n1 = 0, e_n2 = 0;
   if (n_iter > 0) {
-    e_cur = entry(0);
-    if (n_iter > 1) e_next = entry(1);
-    int kt0, fl0;
-    decode(e_cur, kt0, fl0);
-    MODDIT_LOAD_TILE(kt0);
-    MODDIT_STORE_TILE(0);
-  }
-  __syncthreads();
-
-  for (int it = 0; it < n_iter; ++it) {
-    int kt, flags;
-    decode(e_cur, kt, flags);
-    const bool has_next = it + 1 < n_iter;
-    int e_after = 0;
-    if (has_next) {
-      // The entry two tiles ahead is requested before this tile's K/V loads, so waiting
-      // for it later never waits for those loads.
-      if (it + 2 < n_iter) e_after = entry(it + 2);
-      int kn, fn;
-      decode(e_next, kn, fn);
-      MODDIT_LOAD_TILE(kn);
+    const int e0 = entry(0);
+    if (n_iter > 1) e_n1 = entry(1);
+    if (n_iter > 2) e_n2 = entry(2);
+    int kt0, f0;
+    decode(e0, kt0, f0);
+    dma_k(kt0, 0);
+    dma_v(kt0, 0);
+    if (n_iter > 1) {
+      int kt1, f1;
+      decode(e_n1, kt1, f1);
+      dma_k(kt1, 1);
     }
-
-    if (flags & wbit) {
-      const unsigned char* ks = smem + (it & 1) * L::kStage;
-      const unsigned char* vs = ks + L::kKBytes;
-
-      // S^T = K . Q^T, two 32-key halves (rows in key_perm order).
-      f32x16 s0 = f32x16{};
-      f32x16 s1 = f32x16{};
-#pragma unroll
-      for (int c = 0; c < kDChunks; ++c) {
-        const V8 a0 = *reinterpret_cast<const V8*>(ks + c32 * L::kPitchK + c * 32 + half * 16);
-        const V8 a1 =
-            *reinterpret_cast<const V8*>(ks + (32 + c32) * L::kPitchK + c * 32 + half * 16);
-        s0 = E::mma(a0, qf[c], s0);
-        s1 = E::mma(a1, qf[c], s1);
-      }
-
-      if constexpr (kRagged) {
-        const int key0 = kt * kBN;
-        if (key0 + kBN > p.kv_len) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int kr = (i >> 3) * 16 + 8 * half + (i & 7);  // actual key of acc row i
-            if (key0 + kr >= p.kv_len) s0[i] = -INFINITY;
-            if (key0 + 32 + kr >= p.kv_len) s1[i] = -INFINITY;
-          }
-        }
-      }
-
-      float mx = s0[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s0[i]);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s1[i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mxs = mx * p.scale_log2;
-
-      const bool need = mxs > m_run + kRescaleSlack;
-      if (__ballot(need) != 0ull) {
-        const float m_new = need ? mxs : m_run;
-        const float alpha = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-        l_run *= alpha;
-#pragma unroll
-        for (int dsub = 0; dsub < kDSub; ++dsub) oacc[dsub] *= alpha;
-        m_run = m_new;
-      }
-      const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-
-      V8 pb[4];
-      float rs = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], p.scale_log2, -m_use));
-        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], p.scale_log2, -m_use));
-        rs += e0 + e1;
-        pb[i >> 3][i & 7] = static_cast<typename E::elem>(e0);
-        pb[2 + (i >> 3)][i & 7] = static_cast<typename E::elem>(e1);
-      }
-      l_run += rs;
-
-      // O^T += V^T . P^T: lane half h supplies keys 8h..8h+7 of each 16-key chunk.
-#pragma unroll
-      for (int dsub = 0; dsub < kDSub; ++dsub) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const V8 a = *reinterpret_cast<const V8*>(vs + (dsub * 32 + c32) * L::kPitchV + c * 32 +
-                                                    half * 16);
-          oacc[dsub] = E::mma(a, pb[c], oacc[dsub]);
-        }
-      }
-    }
-
-    if (has_next) MODDIT_STORE_TILE((it + 1) & 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    e_cur = e_next;
-    e_next = e_after;
+    act_cur = (f0 & wbit) != 0;
+    if (act_cur) {
+      f32x16 s0, s1;
+      qk(k_ring, s0, s1);
+      float alpha;
+      bool rescale;
+      softmax(s0, s1, kt0, pb, alpha, rescale);
+    }
+    __syncthreads();  // K stage 0 is refilled by the first iteration
+  }
+
+  // Iteration j: S_{j+1} = K_{j+1} Q^T, O += P_j V_j, P_{j+1} = softmax(S_{j+1}); K_{j+2}
+  // and V_{j+1} stream into the stages freed by iteration j-1.
+  bool pend = false;
+  float pend_alpha = 1.f;
+  for (int j = 0; j < n_iter; ++j) {
+    const bool has1 = j + 1 < n_iter;
+    const bool has2 = j + 2 < n_iter;
+    int kt1 = 0, f1 = 0, kt2 = 0, f2 = 0;
+    if (has1) decode(e_n1, kt1, f1);
+    if (has2) decode(e_n2, kt2, f2);
+    int e_n3 = 0;
+    if (j + 3 < n_iter) e_n3 = entry(j + 3);
+    if (has2) dma_k(kt2, j & 1);
+    if (has1) dma_v(kt1, (j + 1) & 1);
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (pend) {
+#pragma unroll
+      for (int dsub = 0; dsub < kDSub; ++dsub) oacc[dsub] *= pend_alpha;
+      pend = false;
+    }
+    const bool act_next = has1 && ((f1 & wbit) != 0);
+    const unsigned char* vs = v_ring + (j & 1) * L::kTileBytes;
+    const unsigned char* ks1 = k_ring + ((j + 1) & 1) * L::kTileBytes;
+    if (act_cur && act_next) {
+      f32x16 s0, s1;
+      qk(ks1, s0, s1);
+      pv(vs, pb);
+      V8 pn[4];
+      softmax(s0, s1, kt1, pn, pend_alpha, pend);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) pb[c] = pn[c];
+    } else {
+      if (act_cur) pv(vs, pb);
+      if (act_next) {
+        f32x16 s0, s1;
+        qk(ks1, s0, s1);
+        softmax(s0, s1, kt1, pb, pend_alpha, pend);
+      }
+    }
+    act_cur = act_next;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    e_n1 = e_n2;
+    e_n2 = e_n3;
+  }
+  if (pend) {
+#pragma unroll
+    for (int dsub = 0; dsub < kDSub; ++dsub) oacc[dsub] *= pend_alpha;
   }
 
   // ---- epilogue ----
@@ -341,9 +414,6 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_kernel(AttnParams p
     }
   }
 }
-
-#undef MODDIT_LOAD_TILE
-#undef MODDIT_STORE_TILE
 
 template <int D, typename E, bool kSparse, bool kRagged>
 int launch_attention_impl(const AttnParams& p, int batch, hipStream_t stream) {
