@@ -72,6 +72,14 @@ int moddit_flash_fwd(const void* q, const void* k, const void* v, void* o, float
  * in ascending order, each encoded as (key_tile << 2) | rows, where bit 0 enables
  * the tile for query rows 0..63 of the query tile and bit 1 for rows 64..127.
  * Rows with no active key tile produce zeros and LSE = -inf.
+ * The tiles live on a grid whose row/column 0 is token grid_origin (-63..0): query
+ * tile t covers tokens grid_origin + 128t .. +127 and key tile j tokens
+ * grid_origin + 64j .. +63. Grid positions outside [0, q_len) / [0, kv_len) are
+ * padding: such keys are masked out and such query rows are not written. A negative
+ * origin lets text-first sequences whose text is not block-aligned (CogVideoX: 226 text
+ * tokens) start both text and video on block boundaries without copying; the
+ * reference rejects such shapes (MoD/mod/triton_flash_sparsity.py:157-160).
+ * n_qtiles must equal ceil((q_len - grid_origin) / 128).
  * Replaces block_sparse_sage2_attn_cuda (MoD/mod/attn_mask.py:306,312-317) as driven
  * by AttentionSparseEngine (attn_mask.py:266-331).
  */
@@ -81,7 +89,7 @@ int moddit_block_sparse_fwd(const void* q, const void* k, const void* v, void* o
                             const int64_t v_strides[3], const int64_t o_strides[3],
                             float softmax_scale, int dtype,
                             const int32_t* counts, const int32_t* entries, int n_qtiles, int cap,
-                            moddit_stream_t stream);
+                            int grid_origin, moddit_stream_t stream);
 
 /*
  * Replayed block sparsity map (video x video blocks), fp16 output (B,H,n,n):
@@ -91,6 +99,9 @@ int moddit_block_sparse_fwd(const void* q, const void* k, const void* v, void* o
  * where round() is round-to-nearest-even to the input dtype and r, c are offset by
  * q_video_offset / k_video_offset. log_threshold = -inf gives an all-zero map.
  * lse: fp32 contiguous (B,H,S). block_size in {64,128}.
+ * The last block may extend past the sequence end (offset + (n-1)*block_size < seq_len):
+ * rows and keys at or beyond seq_len are not counted; the cell is still normalised by
+ * block_size^2. The reference requires whole blocks (cuda_flash_sparsity_kernel.cu:283).
  * Replaces the pybind `sparsity_map` (MoD/mod/cuda_flash_sparsity_kernel.cu:289-334)
  * and the Triton `_sparsity_kernel` (MoD/mod/triton_flash_sparsity.py:28-98).
  */

@@ -21,7 +21,8 @@ from .attn_mask import (
     predict_mask_from_warmup,
     update_warmup,
 )
-from .flash_sparsity import _validate_inputs, cuda_sparsity_map, flash_attn_with_sparsity_map
+from .flash_sparsity import (_validate_inputs, cuda_sparsity_map, flash_attn_with_sparsity_map,
+                             padded_grid)
 from .lstsq import compute_mtm, compute_mts, solve_lstsq
 from .ops import TileList
 from .state import create_adaptive_mask_state, init_warmup_state, is_warmup_complete
@@ -31,5 +32,6 @@ __all__ = [
     "check_bd_values", "choose_topk_lines", "compute_mtm", "compute_mts",
     "create_adaptive_mask_state", "cuda_sparsity_map", "extract_attention_features",
     "flash_attn_with_sparsity_map", "generate_mask_from_lines", "init_warmup_state",
-    "is_warmup_complete", "predict_mask_from_warmup", "solve_lstsq", "update_warmup",
+    "is_warmup_complete", "padded_grid", "predict_mask_from_warmup", "solve_lstsq",
+    "update_warmup",
 ]

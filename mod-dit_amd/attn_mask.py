@@ -30,7 +30,7 @@ from typing import Dict, List, Optional, Tuple
 import torch
 
 from . import _lib, ops
-from .flash_sparsity import flash_attn_with_sparsity_map
+from .flash_sparsity import flash_attn_with_sparsity_map, padded_grid
 from .lstsq import solve_lstsq
 from .state import is_warmup_complete
 
@@ -148,22 +148,38 @@ def choose_topk_lines(history: List[Dict[str, torch.Tensor]], top_k: int = 10,
     return _select_i32(history, top_k, predict_T).long()
 
 
+def _grid(warmup_state: Dict, seq_len: int):
+    """(text_blocks, video_blocks, mask_blocks, origin) of the attention block grid.
+
+    wan / hunyuan / other: the reference's grid (block b = tokens [b*bs, (b+1)*bs)).
+    cogvideox: text-first with text and video each starting on a block boundary, the
+    grid shifted by `origin` <= 0 tokens when the text is not block-aligned
+    (flash_sparsity.padded_grid)."""
+    bs = warmup_state["block_size"]
+    model_type = warmup_state.get("model_type")
+    if model_type == "cogvideox":
+        tb, vb, origin = padded_grid(warmup_state["text_token_num"],
+                                     warmup_state["video_token_num"], bs)
+        return tb, vb, tb + vb, origin
+    tb = warmup_state["text_token_num"] // bs
+    vb = warmup_state["video_token_num"] // bs
+    return tb, vb, seq_len // bs, 0
+
+
 def _generate_mask_and_tiles(warmup_state: Dict, num_heads: int, n: int, blocks_per_frame: int,
                              selected_lines, mode, device, want_tiles=True):
     block_size = warmup_state["block_size"]
-    block_num = n // block_size
-    text_block_num = warmup_state["text_token_num"] // block_size
-    video_block_num = warmup_state["video_token_num"] // block_size
+    text_block_num, video_block_num, block_num, origin = _grid(warmup_state, n)
     model_type = warmup_state.get("model_type")
     layout = _LAYOUTS.get(model_type, _lib.LAYOUT_OTHER)
     if layout == _lib.LAYOUT_WAN:
         nb = video_block_num
     else:
         nb = block_num
-    if layout == _lib.LAYOUT_COGVIDEOX and block_num - text_block_num != video_block_num:
+    if layout == _lib.LAYOUT_COGVIDEOX and block_num * block_size + origin < n:
         raise RuntimeError(
-            f"cogvideox mask: {block_num - text_block_num} video blocks in the sequence "
-            f"but video_token_num gives {video_block_num}"
+            f"cogvideox mask: text {warmup_state['text_token_num']} + video "
+            f"{warmup_state['video_token_num']} tokens do not cover the sequence of {n}"
         )
     if layout == _lib.LAYOUT_HUNYUAN and block_num < video_block_num:
         raise RuntimeError("hunyuan mask: video blocks exceed the sequence")
@@ -178,7 +194,8 @@ def _generate_mask_and_tiles(warmup_state: Dict, num_heads: int, n: int, blocks_
     return ops.mask_from_lines(selected_lines, modes, n=n_video,
                                blocks_per_frame=max(int(blocks_per_frame), 1), layout=layout,
                                nb=nb, text_blocks=text_block_num, block_size=block_size,
-                               union_rows=union, want_mask=True, want_tiles=want_tiles)
+                               union_rows=union, want_mask=True, want_tiles=want_tiles,
+                               grid_origin=origin)
 
 
 def generate_mask_from_lines(warmup_state: Dict, num_heads: int, n: int, blocks_per_frame: int,
@@ -196,7 +213,7 @@ def predict_mask_from_warmup(warmup_state: Dict, n: int, top_k: int = 10,
     blocks_per_frame = warmup_state["blocks_per_frame"]
     if not is_warmup_complete(warmup_state):
         device = torch.device("cuda") if torch.cuda.is_available() else torch.device("cpu")
-        nb = n // warmup_state["block_size"]
+        nb = _grid(warmup_state, n)[2]
         return {
             "mode": ["full"] * num_heads,
             "block_diagonal": [False] * num_heads,
@@ -233,12 +250,13 @@ def _kv_valid(pre_defined_mask: torch.Tensor) -> int:
 
 
 def _engine(query, key, value, mask, tiles, pre_defined_mask, video_token_num, block_size,
-            union_rows):
+            union_rows, grid_origin=0):
     if mask.dim() == 2:
         mask = mask.unsqueeze(0).expand(query.shape[1], -1, -1)
     if pre_defined_mask is None:
         if tiles is None:
-            tiles = ops.mask_to_tiles(mask, block_size, union_rows=union_rows)
+            tiles = ops.mask_to_tiles(mask, block_size, union_rows=union_rows,
+                                      grid_origin=grid_origin)
         out, _ = ops.block_sparse_fwd(query, key, value, tiles)
         return out
     # Hunyuan layout (MoD/mod/attn_mask.py:310-331): video queries run block-sparse over the
@@ -291,7 +309,7 @@ def _video_part(warmup_state: Dict, mask: torch.Tensor) -> torch.Tensor:
     bs = warmup_state["block_size"]
     mt = warmup_state["model_type"]
     if mt == "cogvideox":
-        t = warmup_state["text_token_num"] // bs
+        t = _grid(warmup_state, 0)[0]
         return mask[:, t:, t:]
     if mt == "hunyuan":
         v = warmup_state["video_token_num"] // bs
@@ -381,5 +399,6 @@ def SparseAttentionWithMap(
         tiles = warmup_state.get("_tiles") if warmup_state.get("_tiles_for") is mask else None
         output = _engine(query, key, value, mask, tiles, pre_defined_mask,
                          warmup_state.get("video_token_num", 0), warmup_state["block_size"],
-                         warmup_state.get("tile_rows", "union") == "union")
+                         warmup_state.get("tile_rows", "union") == "union",
+                         grid_origin=_grid(warmup_state, seq_len)[3])
     return output, {"mask": warmup_state["mask"]}

@@ -57,6 +57,7 @@ struct AttnParams {
   int heads;
   int q_len;
   int kv_len;
+  int origin;    // token index of grid row/column 0 (-63..0); see moddit_block_sparse_fwd
   int n_qtiles;
   int n_ktiles;
   float scale_log2;  // softmax_scale * log2(e)
@@ -159,10 +160,11 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
   const int wbit = 1 << (wave >> 1);
 
   // ---- Q fragments (B operand of S^T = K Q^T): lane holds query c32, dims 8*half.. ----
-  const int q_row = qt * kBM + wave * 32 + c32;
+  // Grid rows outside [0, q_len) are padding: they load a clamped row and store nothing.
+  const int q_row = p.origin + qt * kBM + wave * 32 + c32;
   V8 qf[kDChunks];
   {
-    const int r = q_row < p.q_len ? q_row : p.q_len - 1;
+    const int r = q_row < 0 ? 0 : (q_row < p.q_len ? q_row : p.q_len - 1);
     const u32x4* src = reinterpret_cast<const u32x4*>(qb + r * p.q_ss);
 #pragma unroll
     for (int c = 0; c < kDChunks; ++c) qf[c] = as_vec8<V8>(src[2 * c + half]);
@@ -190,6 +192,10 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
   }
   const uint32_t k_tile_bytes = static_cast<uint32_t>(kBN * p.k_ss * 2);
   const uint32_t v_tile_bytes = static_cast<uint32_t>(kBN * p.v_ss * 2);
+  // Grid origin in bytes (two's complement). Keys before token 0 get offsets that wrap
+  // to >= 2^31, beyond every range the buffer descriptors admit, so they load zeros.
+  const uint32_t k_org = static_cast<uint32_t>(p.origin * static_cast<int>(p.k_ss) * 2);
+  const uint32_t v_org = static_cast<uint32_t>(p.origin * static_cast<int>(p.v_ss) * 2);
 
   auto dma_k = [&](int kt, int stage) {
     const uint32_t to = static_cast<uint32_t>(kt) * k_tile_bytes;
@@ -197,7 +203,7 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
     for (int i = 0; i < kWinPerWave; ++i) {
       const uint32_t dst = k_lds + stage * L::kTileBytes + (wave * kWinPerWave + i) * 1024;
       if constexpr (kRagged)
-        lds_dma16(k_rsrc, dst, k_src[i] + to, 0);
+        lds_dma16(k_rsrc, dst, k_src[i] + to + k_org, 0);
       else
         lds_dma16(k_rsrc, dst, k_src[i], to);
     }
@@ -208,7 +214,7 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
     for (int i = 0; i < kWinPerWave; ++i) {
       const uint32_t dst = v_lds + stage * L::kTileBytes + (wave * kWinPerWave + i) * 1024;
       if constexpr (kRagged)
-        lds_dma16(v_rsrc, dst, v_src[i] + to, 0);
+        lds_dma16(v_rsrc, dst, v_src[i] + to + v_org, 0);
       else
         lds_dma16(v_rsrc, dst, v_src[i], to);
     }
@@ -273,13 +279,13 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
   };
   auto softmax = [&](f32x16& s0, f32x16& s1, int kt, V8* pb, float& alpha, bool& rescale) {
     if constexpr (kRagged) {
-      const int key0 = kt * kBN;
-      if (key0 + kBN > p.kv_len) {
+      const int key0 = p.origin + kt * kBN;
+      if (key0 < 0 || key0 + kBN > p.kv_len) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int kr = (i >> 3) * 16 + 8 * half + (i & 7);
-          if (key0 + kr >= p.kv_len) s0[i] = -INFINITY;
-          if (key0 + 32 + kr >= p.kv_len) s1[i] = -INFINITY;
+          const int k0 = key0 + (i >> 3) * 16 + 8 * half + (i & 7);
+          if (k0 < 0 || k0 >= p.kv_len) s0[i] = -INFINITY;
+          if (k0 + 32 < 0 || k0 + 32 >= p.kv_len) s1[i] = -INFINITY;
         }
       }
     }
@@ -392,7 +398,7 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
 
   // ---- epilogue ----
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  if (q_row < p.q_len) {
+  if (q_row >= 0 && q_row < p.q_len) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + q_row * p.o_ss;
 #pragma unroll
@@ -442,8 +448,10 @@ int launch_attention_impl(const AttnParams& p, int batch, hipStream_t stream) {
 
 template <int D, typename E, bool kSparse>
 int launch_attention(const AttnParams& p, int batch, hipStream_t stream) {
-  // Key counts that are a multiple of the tile need no clamping or masking at all.
-  if (p.kv_len % kBN == 0) return launch_attention_impl<D, E, kSparse, false>(p, batch, stream);
+  // Key counts that are a multiple of the tile (on an unshifted grid) need no clamping
+  // or masking at all.
+  if (p.kv_len % kBN == 0 && p.origin == 0)
+    return launch_attention_impl<D, E, kSparse, false>(p, batch, stream);
   return launch_attention_impl<D, E, kSparse, true>(p, batch, stream);
 }
 
@@ -451,7 +459,7 @@ int attention_entry(const void* q, const void* k, const void* v, void* o, float*
                     int heads, int q_len, int kv_len, int head_dim, const int64_t* qs,
                     const int64_t* ks, const int64_t* vs, const int64_t* os, float scale,
                     int dtype, const int32_t* counts, const int32_t* entries, int n_qtiles,
-                    int cap, moddit_stream_t stream) {
+                    int cap, int origin, moddit_stream_t stream) {
   clear_error();
   MODDIT_CHECK_ARG(q && k && v && o, "attention: null tensor pointer");
   MODDIT_CHECK_ARG(qs && ks && vs && os, "attention: null stride array");
@@ -473,12 +481,14 @@ int attention_entry(const void* q, const void* k, const void* v, void* o, float*
     for (int j = 0; j < 3; ++j)
       MODDIT_CHECK_ARG(all[t][j] >= 0 && all[t][j] % 8 == 0,
                        "attention: strides must be non-negative multiples of 8 elements");
+  MODDIT_CHECK_ARG(origin > -kBN && origin <= 0,
+                   "attention: grid_origin must be in (-64, 0], got %d", origin);
   const bool sparse = counts != nullptr;
-  const int nq = (q_len + kBM - 1) / kBM;
+  const int nq = (q_len - origin + kBM - 1) / kBM;
   if (sparse) {
     MODDIT_CHECK_ARG(entries != nullptr, "attention: tile entries missing");
-    MODDIT_CHECK_ARG(n_qtiles == nq, "attention: n_qtiles=%d but q_len=%d needs %d", n_qtiles,
-                     q_len, nq);
+    MODDIT_CHECK_ARG(n_qtiles == nq, "attention: n_qtiles=%d but q_len=%d (grid origin %d) needs %d",
+                     n_qtiles, q_len, origin, nq);
     MODDIT_CHECK_ARG(cap > 0, "attention: cap must be positive");
   }
   if (q_len == 0 || batch == 0 || heads == 0) return MODDIT_OK;
@@ -497,8 +507,9 @@ int attention_entry(const void* q, const void* k, const void* v, void* o, float*
   p.heads = heads;
   p.q_len = q_len;
   p.kv_len = kv_len;
+  p.origin = origin;
   p.n_qtiles = nq;
-  p.n_ktiles = (kv_len + kBN - 1) / kBN;
+  p.n_ktiles = (kv_len - origin + kBN - 1) / kBN;
   p.scale_log2 = scale * 1.4426950408889634f;
   p.counts = counts;
   p.entries = entries;
@@ -543,7 +554,7 @@ extern "C" int moddit_flash_fwd(const void* q, const void* k, const void* v, voi
                                 float softmax_scale, int dtype, moddit_stream_t stream) {
   return moddit::attention_entry(q, k, v, o, lse, batch, heads, q_len, kv_len, head_dim,
                                  q_strides, k_strides, v_strides, o_strides, softmax_scale, dtype,
-                                 nullptr, nullptr, 0, 0, stream);
+                                 nullptr, nullptr, 0, 0, 0, stream);
 }
 
 extern "C" int moddit_block_sparse_fwd(const void* q, const void* k, const void* v, void* o,
@@ -552,12 +563,13 @@ extern "C" int moddit_block_sparse_fwd(const void* q, const void* k, const void*
                                        const int64_t k_strides[3], const int64_t v_strides[3],
                                        const int64_t o_strides[3], float softmax_scale, int dtype,
                                        const int32_t* counts, const int32_t* entries,
-                                       int n_qtiles, int cap, moddit_stream_t stream) {
+                                       int n_qtiles, int cap, int grid_origin,
+                                       moddit_stream_t stream) {
   if (counts == nullptr) {
     moddit::set_error("block_sparse_fwd: counts must not be NULL");
     return MODDIT_EINVAL;
   }
   return moddit::attention_entry(q, k, v, o, lse, batch, heads, q_len, kv_len, head_dim,
                                  q_strides, k_strides, v_strides, o_strides, softmax_scale, dtype,
-                                 counts, entries, n_qtiles, cap, stream);
+                                 counts, entries, n_qtiles, cap, grid_origin, stream);
 }

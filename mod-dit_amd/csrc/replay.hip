@@ -12,7 +12,8 @@
 // Reference semantics: flash_sparsity_replay_kernel
 // (MoD/mod/cuda_flash_sparsity_kernel.cu:41-169): Q scaled in fp32 and rounded to the
 // input dtype (:86-92), fp32 products, strict '<' against lse + log_threshold (:138-143),
-// __float2half_rn of count / block_size^2 (:158-163).
+// __float2half_rn of count / block_size^2 (:158-163). The last video block may run past
+// the sequence end; rows and keys at or beyond seq_len are then not counted.
 #include "common.h"
 
 namespace moddit {
@@ -44,6 +45,8 @@ struct ReplayParams {
   int k_off;
   int nblk;      // video blocks per side
   int block;     // 64 or 128
+  int valid_q;   // video rows that exist: min(nblk*block, seq_len - q_off)
+  int valid_k;   // video keys that exist: min(nblk*block, seq_len - k_off)
   int n_qtiles;  // 128-row tiles of the video region
   int n_ktiles;  // 64-key tiles of the video region
   float scale;
@@ -51,7 +54,7 @@ struct ReplayParams {
   uint32_t k_bytes;  // byte span of one head's video K rows
 };
 
-template <int D, typename E>
+template <int D, typename E, bool kRagged>
 __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p) {
   using L = ReplayLds<D>;
   using V8 = typename E::vec8;
@@ -86,7 +89,8 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
   V8 qf[kDChunks];
   float thr = -INFINITY;
   {
-    const int r = p.q_off + (wave_active ? vrow : 0);
+    const bool row_ok = wave_active && vrow < p.valid_q;
+    const int r = p.q_off + (row_ok ? vrow : 0);
     const u32x4* src = reinterpret_cast<const u32x4*>(qb + r * p.q_ss);
 #pragma unroll
     for (int c = 0; c < kDChunks; ++c) {
@@ -98,13 +102,15 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
                             pack2(e[6], e[7])};
       qf[c] = as_vec8<V8>(packed);
     }
-    thr = p.lse[static_cast<int64_t>(bh) * p.seq_len + r] + p.log_thr;
+    // rows past the sequence end count nothing (no score is below -inf)
+    thr = row_ok ? p.lse[static_cast<int64_t>(bh) * p.seq_len + r] + p.log_thr : -INFINITY;
     // Retire these loads before the loop (see attention.hip).
     __builtin_amdgcn_s_waitcnt(0);
   }
 
   // K rows of the video region through a buffer resource (loop-invariant VGPR offsets,
-  // tile offset in the SGPR offset: every tile is a full in-range tile).
+  // tile offset in the SGPR offset when every tile is a full in-range tile; otherwise in
+  // the range-checked VGPR offset, so rows past the last key load zeros).
   const int k_col = tid % kVecPerRow;
   const int k_row0 = tid / kVecPerRow;
   constexpr int kKRowStep = kThreads / kVecPerRow;
@@ -117,7 +123,12 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
   auto load_tile = [&](int kt) {
     const uint32_t so = static_cast<uint32_t>(kt) * k_tile_bytes;
 #pragma unroll
-    for (int i = 0; i < kKVecs; ++i) kreg[i] = buf_load16(k_rsrc, k_voff, so + i * k_row_step);
+    for (int i = 0; i < kKVecs; ++i) {
+      if constexpr (kRagged)
+        kreg[i] = buf_load16(k_rsrc, k_voff + so + i * k_row_step, 0);
+      else
+        kreg[i] = buf_load16(k_rsrc, k_voff, so + i * k_row_step);
+    }
   };
   auto store_tile = [&](int stage) {
     unsigned char* ks = smem + stage * L::kKBytes;
@@ -150,10 +161,21 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
         s1 = E::mma(a1, qf[c], s1);
       }
       int total = 0;
+      if (kRagged && it * kBN + kBN > p.valid_k) {
+        // keys at or past the sequence end are not counted
+        const int key0 = it * kBN + 4 * half;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        total += __builtin_popcountll(__ballot(s0[i] < thr));
-        total += __builtin_popcountll(__ballot(s1[i] < thr));
+        for (int i = 0; i < 16; ++i) {
+          const int kr = key0 + 8 * (i >> 2) + (i & 3);
+          total += __builtin_popcountll(__ballot(s0[i] < thr && kr < p.valid_k));
+          total += __builtin_popcountll(__ballot(s1[i] < thr && kr + 32 < p.valid_k));
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          total += __builtin_popcountll(__ballot(s0[i] < thr));
+          total += __builtin_popcountll(__ballot(s1[i] < thr));
+        }
       }
       if (lane == 0) cnt[wave * kFlush + (it % kFlush)] = total;
     }
@@ -193,10 +215,10 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
   }
 }
 
-template <int D, typename E>
-int launch_replay(const ReplayParams& p, int batch, hipStream_t stream) {
+template <int D, typename E, bool kRagged>
+int launch_replay_impl(const ReplayParams& p, int batch, hipStream_t stream) {
   using L = ReplayLds<D>;
-  auto kernel = replay_map_kernel<D, E>;
+  auto kernel = replay_map_kernel<D, E, kRagged>;
   static bool configured = false;
   if (!configured) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -212,6 +234,12 @@ int launch_replay(const ReplayParams& p, int batch, hipStream_t stream) {
                      stream, p);
   MODDIT_CHECK_LAUNCH("sparsity_map");
   return MODDIT_OK;
+}
+
+template <int D, typename E>
+int launch_replay(const ReplayParams& p, int batch, hipStream_t stream) {
+  if (p.valid_k == p.n_ktiles * kBN) return launch_replay_impl<D, E, false>(p, batch, stream);
+  return launch_replay_impl<D, E, true>(p, batch, stream);
 }
 
 }  // namespace
@@ -240,8 +268,11 @@ extern "C" int moddit_sparsity_map(const void* q, const void* k, const float* ls
   MODDIT_CHECK_ARG(q_video_offset >= 0 && k_video_offset >= 0,
                    "sparsity_map: video offsets must be non-negative");
   const int64_t vt = static_cast<int64_t>(video_blocks) * block_size;
-  MODDIT_CHECK_ARG(q_video_offset + vt <= seq_len, "sparsity_map: Q video region exceeds sequence length");
-  MODDIT_CHECK_ARG(k_video_offset + vt <= seq_len, "sparsity_map: K video region exceeds sequence length");
+  // the last block may be partial, but must hold at least one token
+  MODDIT_CHECK_ARG(q_video_offset + vt - block_size < seq_len,
+                   "sparsity_map: Q video region exceeds sequence length");
+  MODDIT_CHECK_ARG(k_video_offset + vt - block_size < seq_len,
+                   "sparsity_map: K video region exceeds sequence length");
   MODDIT_CHECK_ARG(batch >= 0 && heads >= 0, "sparsity_map: negative size");
   MODDIT_CHECK_ARG(aligned16(q) && aligned16(k), "sparsity_map: q/k must be 16-byte aligned");
   for (int j = 0; j < 3; ++j)
@@ -264,12 +295,15 @@ extern "C" int moddit_sparsity_map(const void* q, const void* k, const float* ls
   p.k_off = k_video_offset;
   p.nblk = video_blocks;
   p.block = block_size;
+  p.valid_q = static_cast<int>(vt < seq_len - q_video_offset ? vt : seq_len - q_video_offset);
+  p.valid_k = static_cast<int>(vt < seq_len - k_video_offset ? vt : seq_len - k_video_offset);
   p.n_qtiles = static_cast<int>((vt + kBM - 1) / kBM);
   p.n_ktiles = static_cast<int>(vt / kBN);
   p.scale = softmax_scale;
   p.log_thr = log_threshold;
-  const int64_t k_span = (vt - 1) * k_strides[2] * 2 + head_dim * 2;
-  if (k_span > 0x7fffffffLL) {
+  const int64_t k_span = (static_cast<int64_t>(p.valid_k) - 1) * k_strides[2] * 2 + head_dim * 2;
+  const int64_t k_grid = vt * k_strides[2] * 2;  // largest offset a (ragged) tile forms
+  if (k_span > 0x7fffffffLL || k_grid > 0x7fffffffLL) {
     set_error("sparsity_map: one head's K span exceeds 2 GiB of 32-bit offsets");
     return MODDIT_EUNSUPPORTED;
   }

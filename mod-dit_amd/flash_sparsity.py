@@ -20,9 +20,26 @@ import torch
 from . import ops
 
 
+def padded_grid(text_token_num: int, video_token_num: int, block_size: int) -> Tuple[int, int, int]:
+    """Block grid of a text-first (CogVideoX) sequence: (text_blocks, video_blocks, origin).
+
+    Text and video each start on a block boundary: the grid begins `-origin` virtual
+    tokens before token 0 so that the text fills ceil(text/bs) blocks ending exactly where
+    the video begins, and the video fills ceil(video/bs) blocks, the last one padded past
+    the sequence end. Virtual tokens are never attended to and produce no output. For
+    block-aligned text and video this is the reference's own grid (origin 0). The
+    reference rejects unaligned shapes (MoD/mod/triton_flash_sparsity.py:157-160).
+    """
+    tb = -(-text_token_num // block_size)
+    vb = -(-video_token_num // block_size)
+    return tb, vb, text_token_num - tb * block_size
+
+
 def _video_layout(model_type: str, sequence_length: int, video_token_num: int,
                   text_token_num: int, block_size: int) -> Tuple[int, int, int]:
-    """(video_blocks, q_offset, k_offset); MoD/mod/triton_flash_sparsity.py:101-120."""
+    """(video_blocks, q_offset, k_offset); MoD/mod/triton_flash_sparsity.py:101-120.
+
+    cogvideox counts a trailing partial video block (see `padded_grid`)."""
     if model_type == "wan":
         if video_token_num not in (0, sequence_length):
             raise ValueError(
@@ -32,7 +49,7 @@ def _video_layout(model_type: str, sequence_length: int, video_token_num: int,
     if model_type == "hunyuan":
         return video_token_num // block_size, 0, 0
     if model_type == "cogvideox":
-        return video_token_num // block_size, text_token_num, text_token_num
+        return -(-video_token_num // block_size), text_token_num, text_token_num
     raise ValueError(
         f"Unknown model_type: {model_type}, expected 'wan', 'hunyuan', or 'cogvideox'"
     )
@@ -69,9 +86,13 @@ def _validate_inputs(query, key, value, threshold, block_size: int, model_type: 
             raise ValueError(f"video_token_num must be positive for {model_type}")
         video_tokens = video_token_num
     if video_tokens % block_size:
-        raise ValueError(
-            f"video_token_num={video_tokens} must be divisible by block_size={block_size}"
-        )
+        # Text-first sequences whose video ends the sequence get a padded block grid
+        # (`padded_grid`); every other layout keeps the reference's rule.
+        if not (model_type == "cogvideox"
+                and text_token_num + video_token_num == sequence_length):
+            raise ValueError(
+                f"video_token_num={video_tokens} must be divisible by block_size={block_size}"
+            )
     if text_token_num < 0:
         raise ValueError("text_token_num must be non-negative")
     if model_type in ("hunyuan", "cogvideox") and video_token_num + text_token_num > sequence_length:

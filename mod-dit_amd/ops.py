@@ -53,12 +53,15 @@ class TileList:
 
     entries[h, t, i] = (key_tile << 2) | row_bits for i < counts[h, t]; bit 0 enables the
     tile for query rows 0..63 of the query tile, bit 1 for rows 64..127.
+    Tiles sit on a grid whose row/column 0 is token `origin` (-63..0); grid positions
+    before token 0 or past the sequence end are padding (keys masked, rows not written).
     """
 
     counts: torch.Tensor   # (H, n_qtiles) int32
     entries: torch.Tensor  # (H, n_qtiles, cap) int32
     block_size: int
     union_rows: bool
+    origin: int = 0
 
     @property
     def n_qtiles(self) -> int:
@@ -105,7 +108,7 @@ def _attention(q, k, v, scale, return_lse, tiles: TileList | None, out=None):
         if tiles.counts.shape[0] != H:
             raise ValueError(f"tile lists cover {tiles.counts.shape[0]} heads, attention has {H}")
         check(lib.moddit_block_sparse_fwd(*args, tiles.counts.data_ptr(), tiles.entries.data_ptr(),
-                                          tiles.n_qtiles, tiles.cap, _stream(q)),
+                                          tiles.n_qtiles, tiles.cap, int(tiles.origin), _stream(q)),
               "moddit_block_sparse_fwd")
     return out, lse
 
@@ -232,8 +235,10 @@ def _tile_shape(nb: int, block_size: int):
 
 
 def mask_from_lines(sel, mode, *, n, blocks_per_frame, layout, nb, text_blocks, block_size,
-                    union_rows=True, want_mask=True, want_tiles=True):
-    """Bool mask (H,nb,nb) and/or TileList from selected lines (one fused kernel)."""
+                    union_rows=True, want_mask=True, want_tiles=True, grid_origin=0):
+    """Bool mask (H,nb,nb) and/or TileList from selected lines (one fused kernel).
+
+    grid_origin: token index of mask row/column 0 (see TileList)."""
     _require_gpu(sel, mode, what="mask_from_lines")
     H = mode.shape[0]
     sel = sel.to(torch.int32).contiguous()
@@ -246,7 +251,7 @@ def mask_from_lines(sel, mode, *, n, blocks_per_frame, layout, nb, text_blocks, 
     if want_tiles:
         tiles = TileList(torch.empty((H, nq), device=dev, dtype=torch.int32),
                          torch.empty((H, nq, cap), device=dev, dtype=torch.int32),
-                         block_size, bool(union_rows))
+                         block_size, bool(union_rows), int(grid_origin))
     check(_lib.load().moddit_mask_from_lines(
         sel.data_ptr(), H, sel.shape[1], mode.data_ptr(), int(n), int(blocks_per_frame),
         int(layout), int(nb), int(text_blocks), int(block_size), int(bool(union_rows)),
@@ -255,8 +260,11 @@ def mask_from_lines(sel, mode, *, n, blocks_per_frame, layout, nb, text_blocks, 
     return mask, tiles
 
 
-def mask_to_tiles(mask: torch.Tensor, block_size: int, union_rows=True, kv_tiles=None) -> TileList:
-    """TileList of a bool (H, rows, cols) block mask (strided views are read in place)."""
+def mask_to_tiles(mask: torch.Tensor, block_size: int, union_rows=True, kv_tiles=None,
+                  grid_origin=0) -> TileList:
+    """TileList of a bool (H, rows, cols) block mask (strided views are read in place).
+
+    grid_origin: token index of mask row/column 0 (see TileList)."""
     _require_gpu(mask, what="mask_to_tiles")
     if mask.ndim != 3:
         raise ValueError(f"mask must be (H, rows, cols), got {tuple(mask.shape)}")
@@ -271,7 +279,7 @@ def mask_to_tiles(mask: torch.Tensor, block_size: int, union_rows=True, kv_tiles
         kv_tiles = cap
     tiles = TileList(torch.empty((H, nq), device=mask.device, dtype=torch.int32),
                      torch.empty((H, nq, cap), device=mask.device, dtype=torch.int32),
-                     block_size, bool(union_rows))
+                     block_size, bool(union_rows), int(grid_origin))
     check(_lib.load().moddit_mask_to_tiles(mask.data_ptr(), H, rows, cols, mask.stride(0),
                                            mask.stride(1), int(block_size), int(bool(union_rows)),
                                            int(kv_tiles), tiles.counts.data_ptr(),

@@ -16,6 +16,7 @@ __all__ = [
     "choose_topk_lines", "generate_mask_from_lines", "mask_cell", "tiles_from_mask",
     "token_mask_from_tiles", "token_mask_from_blocks", "masked_attention",
     "probability_map", "replay_map", "refresh_merge", "step_phase", "video_layout",
+    "cogvideox_grid",
     "MODE_SPARSE", "MODE_BLOCK_DIAGONAL", "MODE_FULL",
 ]
 
@@ -44,14 +45,26 @@ def fp16_round(x: np.ndarray) -> np.ndarray:
 # layouts (MoD/mod/triton_flash_sparsity.py:101-120)
 # --------------------------------------------------------------------------------------
 def video_layout(model_type: str, S: int, video_tokens: int, text_tokens: int, bs: int):
-    """(video_blocks, q_offset, k_offset)."""
+    """(video_blocks, q_offset, k_offset). cogvideox counts a partial last video block."""
     if model_type == "wan":
         return S // bs, 0, 0
     if model_type == "hunyuan":
         return video_tokens // bs, 0, 0
     if model_type == "cogvideox":
-        return video_tokens // bs, text_tokens, text_tokens
+        return -(-video_tokens // bs), text_tokens, text_tokens
     raise ValueError(f"Unknown model_type: {model_type}")
+
+
+def cogvideox_grid(text_tokens: int, video_tokens: int, bs: int):
+    """(text_blocks, video_blocks, origin) of the padded text-first grid.
+
+    This build's padding rule for shapes the reference rejects
+    (MoD/mod/triton_flash_sparsity.py:157-160): text occupies whole blocks that end where
+    the video starts, video occupies whole blocks from there; grid token g is sequence
+    token g + origin, and grid tokens outside the sequence are padding."""
+    tb = (text_tokens + bs - 1) // bs
+    vb = (video_tokens + bs - 1) // bs
+    return tb, vb, text_tokens - tb * bs
 
 
 # --------------------------------------------------------------------------------------
@@ -257,6 +270,9 @@ def generate_mask_from_lines(sel: np.ndarray, modes: Sequence[int], *, seq_len: 
     block_num = seq_len // block_size
     tb = text_tokens // block_size
     vb = video_tokens // block_size
+    if model_type == "cogvideox":
+        tb, vb, _ = cogvideox_grid(text_tokens, video_tokens, block_size)
+        block_num = tb + vb
     mask = np.ones((H, block_num, block_num), dtype=bool)
     video = np.zeros((H, vb, vb), dtype=bool)
     sel = np.asarray(sel, dtype=np.int64)
@@ -356,19 +372,23 @@ def tiles_from_mask(mask: np.ndarray, block_size: int, union_rows: bool,
     return counts, lists
 
 
-def token_mask_from_tiles(lists, H: int, q_len: int, kv_len: int) -> np.ndarray:
-    """Token-level (H, q_len, kv_len) mask the block-sparse kernel realises."""
+def token_mask_from_tiles(lists, H: int, q_len: int, kv_len: int, origin: int = 0) -> np.ndarray:
+    """Token-level (H, q_len, kv_len) mask the block-sparse kernel realises.
+
+    Tiles sit on a grid whose token 0 is sequence token `origin` (<= 0); the parts of a
+    tile outside the sequence are dropped."""
     m = np.zeros((H, q_len, kv_len), dtype=bool)
     for h in range(H):
         for t, ent in enumerate(lists[h]):
             for e in ent:
                 kt, bits = e >> 2, e & 3
-                k0, k1 = kt * 64, min(kt * 64 + 64, kv_len)
+                k0 = max(kt * 64 + origin, 0)
+                k1 = min(kt * 64 + 64 + origin, kv_len)
                 for half in range(2):
                     if bits & (1 << half):
-                        q0 = t * 128 + 64 * half
-                        q1 = min(q0 + 64, q_len)
-                        if q0 < q1:
+                        q0 = max(t * 128 + 64 * half + origin, 0)
+                        q1 = min(t * 128 + 64 * half + 64 + origin, q_len)
+                        if q0 < q1 and k0 < k1:
                             m[h, q0:q1, k0:k1] = True
     return m
 
@@ -438,19 +458,23 @@ def replay_map(q, k, lse, *, scale: float, log_threshold: float, q_off: int, k_o
     for dyadic inputs), the comparison is strict against fp32(lse + log_threshold)
     (:138-143), and the ratio count/bs^2 is rounded to fp16 (:158-163).
     q, k: (H, S, D) float values already representable in `dtype`; lse: (H, S).
+    The last block may run past S (this build's padded grid): positions >= S count
+    nothing, and the cell is still divided by block_size^2.
     """
     rnd = bf16_round if dtype == "bf16" else fp16_round
     q = np.asarray(q, dtype=np.float32)
     k = np.asarray(k, dtype=np.float32)
-    H = q.shape[0]
+    H, S = q.shape[0], q.shape[1]
     vt = video_blocks * block_size
-    qs = rnd(q[:, q_off:q_off + vt] * np.float32(scale)).astype(np.float64)
-    kk = k[:, k_off:k_off + vt].astype(np.float64)
-    thr = (np.asarray(lse, dtype=np.float32)[:, q_off:q_off + vt] + np.float32(log_threshold)).astype(np.float32)
+    nq = min(vt, S - q_off)
+    nk = min(vt, S - k_off)
+    qs = rnd(q[:, q_off:q_off + nq] * np.float32(scale)).astype(np.float64)
+    kk = k[:, k_off:k_off + nk].astype(np.float64)
+    thr = (np.asarray(lse, dtype=np.float32)[:, q_off:q_off + nq] + np.float32(log_threshold)).astype(np.float32)
     out = np.zeros((H, video_blocks, video_blocks), dtype=np.float16)
     for h in range(H):
-        s = qs[h] @ kk[h].T
-        below = s < thr[h][:, None].astype(np.float64)
+        below = np.zeros((vt, vt), dtype=bool)
+        below[:nq, :nk] = (qs[h] @ kk[h].T) < thr[h][:, None].astype(np.float64)
         cnt = below.reshape(video_blocks, block_size, video_blocks, block_size).sum(axis=(1, 3))
         out[h] = (cnt.astype(np.float32) / np.float32(block_size * block_size)).astype(np.float16)
     return out

@@ -137,6 +137,27 @@ def test_block_sparse_bs128_mask():
     _check_attn(out[0], ref, "sparse bs128")
 
 
+@pytest.mark.parametrize("text,video,D,union", [(50, 450, 64, False), (50, 450, 128, True),
+                                                (226, 1350, 64, False), (100, 200, 128, False)])
+def test_block_sparse_shifted_grid_matches_masked_fp64(text, video, D, union):
+    # text-first sequence with text not block-aligned: the tile grid starts
+    # origin = text - 64*ceil(text/64) tokens before token 0 (this build's padding rule)
+    H, bs = 2, 64
+    S = text + video
+    tb, vb, origin = O.cogvideox_grid(text, video, bs)
+    q, k, v = (_randn((1, H, S, D), 600 + i, torch.bfloat16) for i in range(3))
+    m = _random_block_mask(H, tb + vb, 0.35, 21)
+    m[:, 1, :] = False  # a grid row whose queries attend to nothing
+    tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=union, grid_origin=origin)
+    assert tiles.n_qtiles == -(-(S - origin) // 128)
+    out, lse = ops.block_sparse_fwd(q, k, v, tiles, return_lse=True)
+    _, lists = _tiles_np(tiles)
+    tm = O.token_mask_from_tiles(lists, H, S, S, origin=origin)
+    ref, ref_lse = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), tm, dtype=np.float64)
+    _check_attn(out[0], ref, f"shifted grid text={text} video={video} D={D} union={union}")
+    np.testing.assert_allclose(_np(lse[0]), ref_lse, rtol=0, atol=2e-3)
+
+
 # ====================================================================== sparsity map
 def _layout(model_type, bs):
     # tests/test_flash_sparsity.py:22-25
@@ -170,6 +191,34 @@ def test_sparsity_map_dyadic_bit_exact(model_type, bs, D, dtype):
         ref = O.replay_map(qn[b], kn[b], lse[b], scale=scale, log_threshold=ln_thr, q_off=qo,
                            k_off=ko, video_blocks=vb, block_size=bs, dtype=dt)
         assert np.array_equal(got[b].cpu().numpy(), ref), (model_type, bs, D, dtype, b)
+
+
+@pytest.mark.parametrize("text,video,bs,D,dtype", [
+    (40, 150, 64, 64, torch.bfloat16),    # 3 blocks, the last with 22 tokens
+    (40, 150, 64, 128, torch.float16),
+    (30, 200, 128, 128, torch.bfloat16),  # 2 blocks, the last with 72 tokens
+    (30, 130, 128, 64, torch.bfloat16),   # the last 64-key tile lies wholly past the end
+])
+def test_sparsity_map_partial_last_block_dyadic_bit_exact(text, video, bs, D, dtype):
+    S = text + video
+    rng = np.random.default_rng(S + D)
+    qn = rng.integers(-4, 5, size=(1, 2, S, D)).astype(np.float32) / 8
+    kn = rng.integers(-4, 5, size=(1, 2, S, D)).astype(np.float32) / 8
+    q = torch.from_numpy(qn).to(dtype).to(DEV)
+    k = torch.from_numpy(kn).to(dtype).to(DEV)
+    scale = D ** -0.5
+    s = np.einsum("bhqd,bhkd->bhqk", qn.astype(np.float64), kn.astype(np.float64)) * scale
+    lse = np.log(np.exp(s).sum(-1)).astype(np.float32)
+    vb, qo, ko = O.video_layout("cogvideox", S, video, text, bs)
+    assert qo + (vb - 1) * bs < S < qo + vb * bs
+    ln_thr = math.log(1e-2)
+    got = md.cuda_sparsity_map(q, k, torch.from_numpy(lse).to(DEV), softmax_scale=scale,
+                               log_threshold=ln_thr, q_video_offset=qo, k_video_offset=ko,
+                               video_blocks=vb, block_size=bs)
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    ref = O.replay_map(qn[0], kn[0], lse[0], scale=scale, log_threshold=ln_thr, q_off=qo,
+                       k_off=ko, video_blocks=vb, block_size=bs, dtype=dt)
+    assert np.array_equal(got[0].cpu().numpy(), ref), (text, video, bs, D, dtype)
 
 
 @pytest.mark.parametrize("bs", [64, 128])

@@ -181,6 +181,89 @@ def test_hunyuan_text_tail_with_padding_mask(tile_rows, bs):
             _check_attn(out[0], ref, f"hunyuan map step {step}")
 
 
+@pytest.mark.parametrize("tile_rows", ["exact", "union"])
+def test_cogvideox_unaligned_text_and_video(tile_rows):
+    """CogVideoX layout with 50 text + 450 video tokens at block 64: neither is
+    block-aligned (the reference rejects this, MoD/mod/triton_flash_sparsity.py:157-160).
+    This build's grid starts 14 virtual tokens before the text so that text fills one
+    block and video starts on a block boundary; the video's last block is partial.
+    """
+    H, D, bs = 2, 64, 64
+    text, F, tpf = 50, 3, 150
+    video = F * tpf
+    S = text + video
+    W, T, top_k, thr = 4, 3, 6, 1e-3
+    tb, vb, origin = O.cogvideox_grid(text, video, bs)
+    assert (tb, vb, origin) == (1, 8, -14)
+    st = md.create_adaptive_mask_state("cogvideox", H, video, text, tpf, F, warmup_steps=W,
+                                       top_k=top_k, predict_T=T, threshold=thr, block_size=bs,
+                                       tile_rows=tile_rows)
+    for step in range(W + 2 * T):
+        q, k, v = _structured_qkv(H, 1, S, D, seed=300 + step)
+        qn, kn, vn = (_np(t[0]) for t in (q, k, v))
+        phase = O.step_phase(step, W, T)
+        out, _ = md.SparseAttentionWithMap(q, k, v, st, None, current_step=step,
+                                           use_dense=step < W - 2)
+        if phase != "sparse":
+            ref, _ = O.masked_attention(qn, kn, vn, None, dtype=np.float64)
+            _check_attn(out[0], ref, f"cogvideox {phase} {step}")
+            if phase == "map_fit":
+                # the map covers the partial last video block (reference count bound)
+                _, lse = ops.flash_fwd(q, k, v)
+                rep = O.replay_map(qn, kn, _np(lse[0]), scale=D ** -0.5, log_threshold=math.log(thr),
+                                   q_off=text, k_off=text, video_blocks=vb, block_size=bs)
+                got = st["prev_full_maps"].cpu().numpy().astype(np.float32)
+                assert got.shape == (H, vb, vb)
+                assert (np.abs(got - rep.astype(np.float32)) * bs * bs).max() <= 2.1
+            continue
+        mask = st["mask"].cpu().numpy()
+        assert mask.shape == (H, tb + vb, tb + vb)
+        assert mask[:, :tb, :].all() and mask[:, :, :tb].all()
+        _, lists = O.tiles_from_mask(mask, bs, tile_rows == "union")
+        tm = O.token_mask_from_tiles(lists, H, S, S, origin=origin)
+        assert tm[:, :text, :].all() and tm[:, :, :text].all()  # text rows/cols are dense
+        ref, _ = O.masked_attention(qn, kn, vn, tm, dtype=np.float64)
+        _check_attn(out[0], ref, f"cogvideox sparse {step}", sparse=True)
+
+
+def test_configs1_cogvideox_full_shape():
+    """H=48, d=64, 226 text + 13 x 1350 video tokens, bf16
+    Q/K/V ~ N(0,1)/sqrt(d), block 64, ~75% mask sparsity. The schedule runs at full shape;
+    outputs are checked against fp64 attention under the executed mask for two heads on
+    a row subset that covers the text, the first video block and the partial last one."""
+    H, D, bs = 48, 64, 64
+    text, F, tpf = 226, 13, 1350
+    video = F * tpf
+    S = text + video
+    W, T, thr = 4, 3, 1e-4
+    tb, vb, origin = O.cogvideox_grid(text, video, bs)
+    top_k = round(0.25 * vb)
+    st = md.create_adaptive_mask_state("cogvideox", H, video, text, tpf, F, warmup_steps=W,
+                                       top_k=top_k, predict_T=T, threshold=thr, block_size=bs,
+                                       tile_rows="exact")
+    g = torch.Generator().manual_seed(2024)
+    rows = np.r_[0:300, S - 200:S]
+    heads = [0, 47]
+    for step in range(W + 1):
+        q, k, v = ((torch.randn(1, H, S, D, generator=g) * D ** -0.5).to(torch.bfloat16).to(DEV)
+                   for _ in range(3))
+        phase = O.step_phase(step, W, T)
+        out, _ = md.SparseAttentionWithMap(q, k, v, st, None, current_step=step,
+                                           use_dense=step < W - 2)
+        if phase != "sparse":
+            continue
+        mask = st["mask"].cpu().numpy()
+        assert mask.shape == (H, tb + vb, tb + vb)
+        sparsity = 1.0 - mask[:, tb:, tb:].mean()
+        assert 0.6 < sparsity < 0.9, sparsity
+        _, lists = O.tiles_from_mask(mask[heads], bs, union_rows=False)
+        tm = O.token_mask_from_tiles(lists, len(heads), S, S, origin=origin)[:, rows]
+        qn = _np(q[0, heads])[:, rows]
+        kn, vn = _np(k[0, heads]), _np(v[0, heads])
+        ref, _ = O.masked_attention(qn, kn, vn, tm, dtype=np.float64)
+        _check_attn(out[0, heads][:, rows], ref, "configs[1] sparse", sparse=True)
+
+
 def test_use_dense_and_error_paths():
     H, S, D = 1, 256, 64
     q, k, v = (torch.randn(1, H, S, D).to(torch.bfloat16).to(DEV) for _ in range(3))

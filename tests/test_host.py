@@ -48,6 +48,19 @@ def test_c_abi_rejects_bad_arguments_before_any_launch():
     assert rc == _lib.MODDIT_EUNSUPPORTED and b"head_dim" in lib.moddit_last_error()
     rc = lib.moddit_sparsity_map(16, 16, 16, 16, 1, 1, 128, 64, s, s, 0.1, -1.0, 0, 0, 2, 32, 0, None)
     assert rc == _lib.MODDIT_EINVAL and b"block_size" in lib.moddit_last_error()
+    # the last map block must hold at least one token of the sequence
+    rc = lib.moddit_sparsity_map(16, 16, 16, 16, 1, 1, 128, 64, s, s, 0.1, -1.0, 64, 64, 2, 64, 0,
+                                 None)
+    assert rc == _lib.MODDIT_EINVAL and b"exceeds" in lib.moddit_last_error()
+    # grid origin outside (-64, 0]
+    for origin in (1, -64):
+        rc = lib.moddit_block_sparse_fwd(16, 16, 16, 16, None, 1, 1, 64, 64, 64, s, s, s, s, 0.1, 0,
+                                         16, 16, 1, 1, origin, None)
+        assert rc == _lib.MODDIT_EINVAL and b"grid_origin" in lib.moddit_last_error()
+    # n_qtiles must cover the shifted grid: 64 rows from origin -30 need one 128-row tile
+    rc = lib.moddit_block_sparse_fwd(16, 16, 16, 16, None, 1, 1, 100, 100, 64, s, s, s, s, 0.1, 0,
+                                     16, 16, 1, 1, -30, None)
+    assert rc == _lib.MODDIT_EINVAL and b"needs 2" in lib.moddit_last_error()
     rc = lib.moddit_select_lines(16, 16, 1, 6000, 10, 5, 16, None)
     assert rc == _lib.MODDIT_EINVAL and b"exceeds" in lib.moddit_last_error()
     rc = lib.moddit_mask_from_lines(16, 1, 1, 16, 4, 2, _lib.LAYOUT_WAN, 5, 0, 64, 1,

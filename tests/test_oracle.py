@@ -208,6 +208,69 @@ def test_tiles_realise_the_mask(nb, bs):
             assert keys == sorted(keys) and len(keys) == counts[h, t]
 
 
+@pytest.mark.parametrize("text,video,bs", [(50, 450, 64), (226, 1350, 64), (100, 700, 128),
+                                           (128, 512, 64)])
+def test_cogvideox_grid_puts_text_and_video_on_block_boundaries(text, video, bs):
+    tb, vb, origin = O.cogvideox_grid(text, video, bs)
+    assert -bs < origin <= 0 and (origin == 0) == (text % bs == 0)
+    assert tb * bs + origin == text  # video starts on grid block tb
+    assert (tb - 1) * bs < text - origin <= tb * bs and (vb - 1) * bs < video <= vb * bs
+
+
+@pytest.mark.parametrize("text,video", [(50, 450), (30, 300), (64, 130)])
+def test_padded_grid_tiles_realise_the_cropped_block_mask(text, video):
+    # the tile mask on a shifted grid equals the grid-token expansion of the block mask,
+    # cropped to the sequence: built here with np.repeat and slicing, not with the tiles
+    rng = np.random.default_rng(text + video)
+    tb, vb, origin = O.cogvideox_grid(text, video, 64)
+    nb, S = tb + vb, text + video
+    mask = rng.random((2, nb, nb)) < 0.4
+    _, exact = O.tiles_from_mask(mask, 64, union_rows=False)
+    tm = O.token_mask_from_tiles(exact, 2, S, S, origin=origin)
+    grid = O.token_mask_from_blocks(mask, 64)
+    assert np.array_equal(tm, grid[:, -origin:-origin + S, -origin:-origin + S])
+
+
+def test_generate_mask_cogvideox_padded_grid_equals_cell_definition():
+    rng = np.random.default_rng(77)
+    text, video, bs, bpf, H = 50, 450, 64, 2, 3
+    tb, n, _ = O.cogvideox_grid(text, video, bs)
+    sel = rng.integers(0, 3 * n - 1, size=(H, 4))
+    modes = [O.MODE_SPARSE, O.MODE_BLOCK_DIAGONAL, O.MODE_SPARSE]
+    m = O.generate_mask_from_lines(sel, modes, seq_len=text + video, block_size=bs,
+                                   video_tokens=video, text_tokens=text, bpf=bpf,
+                                   model_type="cogvideox")
+    assert m.shape == (H, tb + n, tb + n)
+    assert m[:, :tb, :].all() and m[:, :, :tb].all()
+    for h in range(H):
+        for i in range(n):
+            for j in range(n):
+                assert m[h, tb + i, tb + j] == O.mask_cell(sel[h], modes[h], n, bpf, i, j)
+
+
+def test_replay_partial_last_block_counts_only_tokens_in_the_sequence():
+    # brute force with explicit loops over the valid rectangle of every cell
+    rng = np.random.default_rng(5)
+    H, D, bs, off, video = 1, 64, 64, 40, 150  # 3 blocks, the last holds 22 tokens
+    S = off + video
+    q = rng.integers(-4, 5, size=(H, S, D)).astype(np.float32) / 8
+    k = rng.integers(-4, 5, size=(H, S, D)).astype(np.float32) / 8
+    s = np.einsum("hqd,hkd->hqk", q.astype(np.float64), k.astype(np.float64)) / 8
+    lse = np.log(np.exp(s).sum(-1)).astype(np.float32)
+    vb = 3
+    rep = O.replay_map(q, k, lse, scale=1 / 8, log_threshold=math.log(1e-2), q_off=off,
+                       k_off=off, video_blocks=vb, block_size=bs)
+    thr = lse[0] + np.float32(math.log(1e-2))
+    for i in range(vb):
+        for j in range(vb):
+            c = 0
+            for r in range(i * bs, min((i + 1) * bs, video)):
+                for cc in range(j * bs, min((j + 1) * bs, video)):
+                    c += s[0, off + r, off + cc] < thr[off + r]
+            assert rep[0, i, j] == np.float16(np.float32(c) / np.float32(bs * bs)), (i, j)
+    assert rep[0, 2, 2] * bs * bs <= 22 * 22
+
+
 # ------------------------------------------------------------------ attention / map --
 def test_masked_attention_all_true_is_dense_and_local_is_blockwise():
     rng = np.random.default_rng(30)
