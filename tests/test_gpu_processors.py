@@ -1,0 +1,280 @@
+"""Processor-level drop-in test (GPU only).
+
+Mock diffusers-style `Attention` modules (QKV projections, RMS QK-norm, rotary embedding,
+Hunyuan's encoder stream and padding mask) driven by processors that restate the
+reference call sites around `SparseAttentionWithMap`:
+
+- Wan (MoD/models/wan/attention_processor.py:118-169): the pipeline sets
+  `processor.current_step = i` for every block each step (MoD/models/wan/
+  sparse_pipeline.py:229-230); the processor computes the `use_dense` gate, transposes
+  (B,S,H,D) projections to (B,H,S,D) views without copying, and alternates the
+  classifier-free-guidance states warmup_state[0] / warmup_state[1] on consecutive
+  calls (`self.neg`), passing `use_cuda` and `use_dense` through **kwargs.
+- Hunyuan (MoD/models/hunyuan/attention_processor.py:110-181): video and encoder
+  streams are concatenated, dense steps use SDPA with the padding mask, sparse steps
+  pass `pre_defined_mask = attention_mask[0, 0].expand(S, S)`, and the processor
+  increments its own `current_step` after every call (:181).
+
+Every attention call is checked against fp64 attention under the mask the state held
+for that call, and the two CFG states are checked to evolve
+independently.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import mod_dit_amd as md
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _check(out, ref, tag, sparse=False):
+    err = np.abs(_np(out).astype(np.float64) - ref)
+    bound = 2e-2 + (2.0 ** -9) * np.abs(ref) if sparse else 2e-2
+    assert np.all(err <= bound) and err.mean() <= 2e-3, (tag, err.max(), err.mean())
+
+
+class MockAttention(torch.nn.Module):
+    """The parts of diffusers' Attention the processors touch."""
+
+    def __init__(self, dim, heads, encoder_dim=None, seed=0):
+        super().__init__()
+        torch.manual_seed(seed)
+        self.heads = heads
+        self.to_q = torch.nn.Linear(dim, dim)
+        self.to_k = torch.nn.Linear(dim, dim)
+        self.to_v = torch.nn.Linear(dim, dim)
+        self.norm_q = torch.nn.RMSNorm(dim, eps=1e-6)
+        self.norm_k = torch.nn.RMSNorm(dim, eps=1e-6)
+        self.to_out = torch.nn.ModuleList([torch.nn.Linear(dim, dim), torch.nn.Dropout(0.0)])
+        if encoder_dim is not None:
+            self.add_q_proj = torch.nn.Linear(encoder_dim, dim)
+            self.add_k_proj = torch.nn.Linear(encoder_dim, dim)
+            self.add_v_proj = torch.nn.Linear(encoder_dim, dim)
+            self.to_add_out = torch.nn.Linear(dim, encoder_dim)
+        else:
+            self.add_q_proj = None
+
+
+def _rotary(S, D, base=10000.0):
+    pos = torch.arange(S, dtype=torch.float64)[:, None]
+    inv = base ** (-torch.arange(0, D, 2, dtype=torch.float64) / D)
+    ang = (pos * inv).repeat_interleave(2, dim=-1)  # (S, D)
+    return ang.cos().float(), ang.sin().float()
+
+
+def _apply_rotary_interleaved(x, cos, sin):
+    # wan/attention_processor.py:79-90: pairs (0,1),(2,3),... rotated in place
+    x1, x2 = x.unflatten(-1, (-1, 2)).unbind(-1)
+    c, s = cos[..., 0::2], sin[..., 1::2]
+    out = torch.empty_like(x)
+    out[..., 0::2] = x1 * c - x2 * s
+    out[..., 1::2] = x1 * s + x2 * c
+    return out.type_as(x)
+
+
+class Recorder:
+    """Wraps SparseAttentionWithMap: records inputs, the state's mask before the call and
+    the output, so the test can recompute each call with the oracle."""
+
+    def __init__(self):
+        self.calls = []
+
+    def __call__(self, query, key, value, warmup_state, logger, **kw):
+        mask_before = warmup_state.get("mask")
+        out, info = md.SparseAttentionWithMap(query, key, value, warmup_state, logger, **kw)
+        self.calls.append(dict(q=query, k=key, v=value, state=warmup_state, out=out,
+                               mask=mask_before, step=kw.get("current_step", 0),
+                               use_dense=kw.get("use_dense", False),
+                               pdm=kw.get("pre_defined_mask")))
+        return out, info
+
+
+class WanProcessor:
+    """Restatement of the Wan self-attention call site (attention_processor.py:60-169)."""
+
+    def __init__(self, warmup_states, layer_idx, dense_block, attention_fn):
+        self.warmup_state = warmup_states
+        self.layer_idx = layer_idx
+        self.dense_block = dense_block
+        self.current_step = 0
+        self.neg = False
+        self.use_cuda = True
+        self.attention_fn = attention_fn
+
+    def __call__(self, attn, hidden_states, rotary_emb):
+        query = attn.norm_q(attn.to_q(hidden_states))
+        key = attn.norm_k(attn.to_k(hidden_states))
+        value = attn.to_v(hidden_states)
+        query = query.unflatten(2, (attn.heads, -1))
+        key = key.unflatten(2, (attn.heads, -1))
+        value = value.unflatten(2, (attn.heads, -1))
+        query = _apply_rotary_interleaved(query, *rotary_emb)
+        key = _apply_rotary_interleaved(key, *rotary_emb)
+        use_dense = (self.layer_idx < self.dense_block or self.warmup_state is None
+                     or self.current_step < self.warmup_state[0]["warmup_steps"] - 2)
+        query, key, value = (t.transpose(1, 2) for t in (query, key, value))
+        state = self.warmup_state[1 if self.neg else 0]
+        hidden, _ = self.attention_fn(query=query, key=key, value=value, warmup_state=state,
+                                      logger=None, current_step=self.current_step,
+                                      layer_idx=self.layer_idx, use_cuda=self.use_cuda,
+                                      use_dense=use_dense)
+        self.neg = not self.neg
+        hidden = hidden.transpose(1, 2).flatten(2, 3).type_as(query)
+        return attn.to_out[1](attn.to_out[0](hidden))
+
+
+class HunyuanProcessor:
+    """Restatement of the HunyuanVideo call site (attention_processor.py:40-181)."""
+
+    def __init__(self, warmup_state, layer_idx, dense_block, dense_timestep, attention_fn):
+        self.warmup_state = warmup_state
+        self.layer_idx = layer_idx
+        self.dense_block = dense_block
+        self.dense_timestep = dense_timestep
+        self.current_step = 0
+        self.attention_fn = attention_fn
+        self.dense_outputs = []
+
+    def __call__(self, attn, hidden_states, encoder_hidden_states, attention_mask, rotary_emb):
+        query = attn.to_q(hidden_states).unflatten(2, (attn.heads, -1)).transpose(1, 2)
+        key = attn.to_k(hidden_states).unflatten(2, (attn.heads, -1)).transpose(1, 2)
+        value = attn.to_v(hidden_states).unflatten(2, (attn.heads, -1)).transpose(1, 2)
+        query = _apply_rotary_interleaved(query, *rotary_emb)
+        key = _apply_rotary_interleaved(key, *rotary_emb)
+        eq = attn.add_q_proj(encoder_hidden_states).unflatten(2, (attn.heads, -1)).transpose(1, 2)
+        ek = attn.add_k_proj(encoder_hidden_states).unflatten(2, (attn.heads, -1)).transpose(1, 2)
+        ev = attn.add_v_proj(encoder_hidden_states).unflatten(2, (attn.heads, -1)).transpose(1, 2)
+        query = torch.cat([query, eq], dim=2)
+        key = torch.cat([key, ek], dim=2)
+        value = torch.cat([value, ev], dim=2)
+        use_dense = (self.current_step < self.dense_timestep or self.layer_idx < self.dense_block
+                     or self.warmup_state is None
+                     or self.current_step < self.warmup_state["warmup_steps"] - 2)
+        if use_dense:
+            # the processor's own SDPA (computed in fp32 here)
+            hidden = torch.nn.functional.scaled_dot_product_attention(
+                query.float(), key.float(), value.float(), attn_mask=attention_mask,
+                dropout_p=0.0, is_causal=False).to(query.dtype)
+            self.dense_outputs.append(hidden)
+        else:
+            pdm = attention_mask[0, 0].expand(query.shape[2], query.shape[2]).contiguous()
+            hidden, _ = self.attention_fn(query=query, key=key, value=value, pre_defined_mask=pdm,
+                                          warmup_state=self.warmup_state, logger=None,
+                                          current_step=self.current_step,
+                                          layer_idx=self.layer_idx)
+        hidden = hidden.transpose(1, 2).flatten(2, 3).to(query.dtype)
+        n_enc = encoder_hidden_states.shape[1]
+        hidden, enc = hidden[:, :-n_enc], hidden[:, -n_enc:]
+        hidden = attn.to_out[1](attn.to_out[0](hidden))
+        enc = attn.to_add_out(enc)
+        self.current_step += 1
+        return hidden, enc
+
+
+def _expected(call, layout, bs, tile_rows, video, text, valid=None):
+    """fp64 attention of one recorded call under the mask its state held."""
+    q, k, v = (_np(call[n][0]) for n in ("q", "k", "v"))
+    st = call["state"]
+    H, S = q.shape[0], q.shape[1]
+    W, T = st["warmup_steps"], st["predict_T"]
+    phase = "dense" if call["use_dense"] else O.step_phase(call["step"], W, T)
+    if phase != "sparse":
+        tm = None
+        if phase == "dense" and valid is not None:
+            tm = np.zeros((H, S, S), bool)
+            tm[:, :, :valid] = True
+        return O.masked_attention(q, k, v, tm, dtype=np.float64)[0], False
+    mask = call["mask"].cpu().numpy()
+    union = tile_rows == "union"
+    if layout == "hunyuan":
+        nbv = video // bs
+        kv_tiles = (valid + 63) // 64
+        _, lists = O.tiles_from_mask(mask[:, :nbv, :], bs, union, kv_tiles=kv_tiles)
+        tm = np.zeros((H, S, S), bool)
+        tm[:, :video, :] = O.token_mask_from_tiles(lists, H, video, S)
+        tm[:, video:, :valid] = True
+    else:
+        _, lists = O.tiles_from_mask(mask, bs, union)
+        tm = O.token_mask_from_tiles(lists, H, S, S)
+    return O.masked_attention(q, k, v, tm, dtype=np.float64)[0], True
+
+
+@pytest.mark.parametrize("tile_rows", ["exact", "union"])
+def test_wan_processor_cfg_alternation_and_step_counter(tile_rows):
+    H, D, F, tpf, bs = 2, 64, 3, 512, 64
+    S, C = F * tpf, H * D
+    W, T, top_k, thr, steps = 4, 3, 40, 1e-3, 10
+    states = [md.create_adaptive_mask_state("wan", H, S, 0, tpf, F, warmup_steps=W, top_k=top_k,
+                                            predict_T=T, threshold=thr, block_size=bs,
+                                            tile_rows=tile_rows) for _ in range(2)]
+    attn = MockAttention(C, H, seed=1).to(DEV).to(torch.bfloat16)
+    rec = Recorder()
+    procs = [WanProcessor(states, layer_idx=li, dense_block=1, attention_fn=rec) for li in range(2)]
+    rot = tuple(t[None, :, None, :].to(DEV) for t in _rotary(S, D))  # (1, S, 1, D) for (B,S,H,D)
+    g = torch.Generator().manual_seed(3)
+    pos = torch.randn(S, C, generator=g)
+    with torch.no_grad():
+        for i in range(steps):
+            for p in procs:  # the pipeline sets the step on every block (sparse_pipeline.py:229-230)
+                p.current_step = i
+            for branch in range(2):  # cond, then uncond: one transformer pass each
+                x = (torch.randn(1, S, C, generator=g) * 0.5 + pos).to(torch.bfloat16).to(DEV)
+                for p in procs:
+                    out = p(attn, x, rot)
+                    assert out.shape == (1, S, C) and out.dtype == torch.bfloat16
+    # layer 0 is a dense block: use_dense on every call; layer 1 follows the schedule
+    assert len(rec.calls) == steps * 2 * 2
+    for n, call in enumerate(rec.calls):
+        i, branch, layer = n // 4, (n // 2) % 2, n % 2
+        assert call["step"] == i
+        assert call["state"] is states[branch]
+        assert call["use_dense"] == (layer == 0 or i < W - 2)
+        assert call["q"].stride(2) == H * D  # (B,S,H,D) storage viewed as (B,H,S,D)
+        ref, sparse = _expected(call, "wan", bs, tile_rows, S, 0)
+        _check(call["out"][0], ref, f"wan step {i} branch {branch} layer {layer}", sparse)
+    # the two CFG states saw different inputs and evolved independently
+    assert states[0]["mask"] is not None and states[1]["mask"] is not None
+    f0, f1 = (st["features_history"][-1]["_x"] for st in states)
+    assert not torch.equal(f0, f1)
+
+
+def test_hunyuan_processor_padding_mask_and_self_incrementing_step():
+    H, D, F, tpf, bs = 2, 64, 2, 512, 64
+    video, text, valid_text = F * tpf, 256, 150
+    S, C, Ce = video + text, H * D, 96
+    W, T, top_k, thr, calls = 4, 3, 30, 1e-3, 9
+    st = md.create_adaptive_mask_state("hunyuan", H, video, text, tpf, F, warmup_steps=W,
+                                       top_k=top_k, predict_T=T, threshold=thr, block_size=bs,
+                                       tile_rows="exact")
+    attn = MockAttention(C, H, encoder_dim=Ce, seed=2).to(DEV).to(torch.bfloat16)
+    rec = Recorder()
+    proc = HunyuanProcessor(st, layer_idx=3, dense_block=1, dense_timestep=1, attention_fn=rec)
+    rot = tuple(t.to(DEV) for t in _rotary(video, D))
+    valid = video + valid_text
+    amask = torch.zeros(1, 1, 1, S, dtype=torch.bool, device=DEV)
+    amask[..., :valid] = True
+    g = torch.Generator().manual_seed(4)
+    pos = torch.randn(video, C, generator=g)
+    with torch.no_grad():
+        for n in range(calls):
+            x = (torch.randn(1, video, C, generator=g) * 0.5 + pos).to(torch.bfloat16).to(DEV)
+            e = torch.randn(1, text, Ce, generator=g).to(torch.bfloat16).to(DEV)
+            out, enc = proc(attn, x, e, amask, rot)
+            assert out.shape == (1, video, C) and enc.shape == (1, text, Ce)
+            assert proc.current_step == n + 1  # incremented by the processor itself (:181)
+    # steps 0-1 took the processor's SDPA (dense_timestep=1 and step < W-2); the rest ours
+    assert len(proc.dense_outputs) == W - 2
+    assert [c["step"] for c in rec.calls] == list(range(W - 2, calls))
+    for call in rec.calls:
+        assert call["pdm"].shape == (S, S) and bool(call["pdm"][0, :valid].all())
+        assert not bool(call["pdm"][:, valid:].any())
+        ref, sparse = _expected(call, "hunyuan", bs, "exact", video, text, valid=valid)
+        _check(call["out"][0], ref, f"hunyuan step {call['step']}", sparse)
