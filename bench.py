@@ -453,13 +453,19 @@ def main(argv=None):
     overhead_ms = sorted(ov)[len(ov) // 2]
 
     log("timing replay map pass")
-    lse = torch.empty((1, H, N), device=q.device, dtype=torch.float32)
     _, lse = ops.flash_fwd(q, k, v, return_lse=True, out=dense_out)
     rp = time_events(lambda: ops.sparsity_map(q, k, lse, softmax_scale=D ** -0.5,
                                               log_threshold=math.log(args.threshold),
                                               q_video_offset=0, k_video_offset=0,
                                               video_blocks=N // bs, block_size=bs), 2)
     replay_ms = min(rp)
+    # the single-kernel alternative (dense pass + map), for comparison only
+    fm = time_events(lambda: ops.flash_fwd_map(q, k, v, softmax_scale=D ** -0.5,
+                                               log_threshold=math.log(args.threshold),
+                                               video_offset=0, video_blocks=N // bs,
+                                               block_size=bs, return_lse=False,
+                                               out=dense_out), 2)
+    map_step_fused_ms = min(fm)
 
     cpu = None
     if not args.no_cpu:
@@ -497,6 +503,8 @@ def main(argv=None):
         "mask_overhead_ms": round(overhead_ms, 4),
         "mask_overhead_frac_of_dense": round(overhead_ms / dense_ms, 5),
         "replay_ms": round(replay_ms, 3),
+        "map_step_ms": round(dense_ms + replay_ms, 3),
+        "map_step_fused_ms": round(map_step_fused_ms, 3),
         "mask_overhead_amortized_ms": round(overhead_ms + replay_ms / 10.0, 4),
         "speedup_incl_mask": round(dense_ms / (ms + overhead_ms), 3),
         "roofline": {

@@ -92,6 +92,23 @@ int moddit_block_sparse_fwd(const void* q, const void* k, const void* v, void* o
                             int grid_origin, moddit_stream_t stream);
 
 /*
+ * Dense attention and the replayed sparsity map in one kernel: every workgroup runs
+ * the dense pass of moddit_flash_fwd for its 128 query rows (O, and LSE when lse is not
+ * NULL), then, with the rows' final LSE still in registers, sweeps the video key tiles
+ * again and writes the map cells of moddit_sparsity_map for those rows (same counts,
+ * same fp16 rounding, same partial-last-block rule). Self-attention: q_len = kv_len =
+ * seq_len, and the video region starts at video_offset for queries and keys alike.
+ * Replaces the two passes of flash_attn_with_sparsity_map
+ * (MoD/mod/triton_flash_sparsity.py:274-341: flash_attn_func, then sparsity_map).
+ */
+int moddit_flash_fwd_map(const void* q, const void* k, const void* v, void* o, float* lse,
+                         void* map_out, int batch, int heads, int seq_len, int head_dim,
+                         const int64_t q_strides[3], const int64_t k_strides[3],
+                         const int64_t v_strides[3], const int64_t o_strides[3],
+                         float softmax_scale, float log_threshold, int video_offset,
+                         int video_blocks, int block_size, int dtype, moddit_stream_t stream);
+
+/*
  * Replayed block sparsity map (video x video blocks), fp16 output (B,H,n,n):
  *   map[b,h,i,j] = fp16_rn( #{(r,c) in block (i,j) :
  *                   fp32(sum_d round(q[r,d]*scale) * k[c,d]) < lse[r] + log_threshold}

@@ -34,6 +34,9 @@ _SIGNATURES = {
     "moddit_block_sparse_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                                      _c_i64p, _c_i64p, _c_i64p, _c_i64p, _f, _i,
                                      _vp, _vp, _i, _i, _i, _vp]),
+    "moddit_flash_fwd_map": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
+                                  _c_i64p, _c_i64p, _c_i64p, _c_i64p, _f, _f, _i, _i, _i, _i,
+                                  _vp]),
     "moddit_sparsity_map": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _c_i64p, _c_i64p,
                                  _f, _f, _i, _i, _i, _i, _i, _vp]),
     "moddit_mts": (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),

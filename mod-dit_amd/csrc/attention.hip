@@ -66,6 +66,15 @@ struct AttnParams {
   int cap;
   uint32_t k_bytes;  // byte span of one head's K rows [0, kv_len)
   uint32_t v_bytes;
+  // fused sparsity map (map != nullptr only for the kMap kernels)
+  uint16_t* map;     // fp16 (B*H, map_nblk, map_nblk)
+  int map_q_off;     // token of video row 0 (== key offset)
+  int map_kt0;       // grid key tile holding video key 0
+  int map_nblk;      // video blocks per side
+  int map_block;     // 64 or 128
+  int map_valid;     // video tokens that exist: min(map_nblk*map_block, seq_len - map_q_off)
+  float map_scale;   // softmax scale applied to q before rounding
+  float map_log_thr; // ln(threshold)
 };
 
 // K rows are stored in LDS in the order pi(r): inside every 16-row chunk the row groups
@@ -94,8 +103,14 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 // explicitly (s_waitcnt vmcnt(0) + barrier) before any wave reads the written stage;
 // vmcnt waits the compiler emits for its own loads stay correct because vector loads
 // retire in issue order.
+// The hazard recognizer does not look inside inline asm, so the asm supplies the wait
+// states itself: an LDS DMA must not issue in the cycle after an SALU write of m0 (the
+// compiler writes m0 right before the asm), and a VMEM instruction needs 5 wait states
+// after a VALU write (v_readlane / v_readfirstlane, e.g. a spilled descriptor being
+// reloaded) of an SGPR it reads. Without them the load can pick up the previous m0 or a
+// stale descriptor word and land in, or come from, the wrong place.
 __device__ __forceinline__ void lds_dma16(u32x4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                :
                : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds)
                : "memory");
@@ -119,7 +134,16 @@ __device__ __forceinline__ s16x4 lds_read_tr16(const unsigned char* a) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(a));
 }
 
-template <int D, typename E, bool kSparse, bool kRagged>
+// Map flush granularity of the fused map pass (key tiles per flush; the LDS count ring
+// holds two flushes so that a flush never races the next tiles' counts).
+constexpr int kMapFlush = 64;
+constexpr int kMapCountBytes = 4 * 2 * kMapFlush * 4;  // int per (wave, ring slot)
+
+// s_waitcnt with lgkmcnt(0) and vmcnt(n), n < 16 (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
+// lgkmcnt[11:8]); expcnt is left unconstrained.
+#define MODDIT_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(0x0070 | (n))
+
+template <int D, typename E, bool kSparse, bool kRagged, bool kMap = false>
 __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fwd_kernel(AttnParams p) {
   using L = AttnLds<D>;
   using V8 = typename E::vec8;
@@ -419,17 +443,126 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
       p.lse[li] = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
     }
   }
+
+  if constexpr (kMap) {
+    // ---- fused sparsity map: with this tile's final LSE in registers, sweep the video
+    // key tiles again with bf16(q*scale) and count the scores below lse + ln(threshold)
+    // (MoD/mod/cuda_flash_sparsity_kernel.cu:82-163). The grid origin puts every video
+    // block on this tile's 64/128-row boundaries, so the counts of waves (0,1) / (2,3)
+    // (or all four, for 128-blocks) are whole map cells.
+    const int vrow_tile = p.origin + qt * kBM - p.map_q_off;  // multiple of 128
+    if (vrow_tile + kBM <= 0 || vrow_tile >= p.map_valid) return;  // uniform per workgroup
+    const int vrow = vrow_tile + wave * 32 + c32;
+    const bool row_ok = vrow >= 0 && vrow < p.map_valid;
+    // the LSE exactly as stored above
+    const float lse_row = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+    const float thr = row_ok ? lse_row + p.map_log_thr : -INFINITY;
+    {
+      // q scaled in fp32 and rounded to the storage type (reference :86-92)
+      const int r = q_row < 0 ? 0 : (q_row < p.q_len ? q_row : p.q_len - 1);
+      const u32x4* src = reinterpret_cast<const u32x4*>(qb + r * p.q_ss);
+#pragma unroll
+      for (int c = 0; c < kDChunks; ++c) {
+        const u32x4 raw = src[2 * c + half];
+        uint16_t e[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) e[j] = E::from_float(E::to_float(u16_at(raw, j)) * p.map_scale);
+        qf[c] = as_vec8<V8>(u32x4{pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]),
+                                  pack2(e[6], e[7])});
+      }
+    }
+    // K-only pass: all four 16 KB stages of the K and V rings form one K ring, filled
+    // three tiles ahead; the count ring sits past them.
+    int* cnt = reinterpret_cast<int*>(smem + 4 * L::kTileBytes);
+    const int n_vt = p.map_nblk * p.map_block / kBN;
+    uint16_t* out_bh = p.map + static_cast<int64_t>(bh) * p.map_nblk * p.map_nblk;
+    const float inv_area = 1.0f / static_cast<float>(p.map_block * p.map_block);
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+      if (t < n_vt) dma_k(p.map_kt0 + t, t);
+    // tile 0 has landed once at most the two later tiles' DMAs are outstanding
+    if (n_vt >= 3)
+      MODDIT_WAIT_VM_LGKM0(8);
+    else
+      MODDIT_WAIT_VM_LGKM0(0);
+    __syncthreads();
+    for (int j = 0; j < n_vt; ++j) {
+      // stage (j+3)%4 held tile j-1, read in the previous iteration (barrier since)
+      if (j + 3 < n_vt) dma_k(p.map_kt0 + j + 3, (j + 3) & 3);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x16 s0, s1;
+      qk(k_ring + (j & 3) * L::kTileBytes, s0, s1);
+      int total = 0;
+      if (j * kBN + kBN > p.map_valid) {
+        // keys past the sequence end are not counted
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kr = j * kBN + (i >> 3) * 16 + 8 * half + (i & 7);
+          total += __builtin_popcountll(__ballot(s0[i] < thr && kr < p.map_valid));
+          total += __builtin_popcountll(__ballot(s1[i] < thr && kr + 32 < p.map_valid));
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          total += __builtin_popcountll(__ballot(s0[i] < thr));
+          total += __builtin_popcountll(__ballot(s1[i] < thr));
+        }
+      }
+      if (lane == 0) cnt[wave * 2 * kMapFlush + (j % (2 * kMapFlush))] = total;
+      // tile j+1 must have landed; the DMAs of tiles j+2 and j+3 (and any map stores,
+      // which are younger than tile j+1's DMA) may stay outstanding
+      if (j + 3 < n_vt)
+        MODDIT_WAIT_VM_LGKM0(8);
+      else if (j + 2 < n_vt)
+        MODDIT_WAIT_VM_LGKM0(4);
+      else
+        MODDIT_WAIT_VM_LGKM0(0);
+      __syncthreads();
+      const int slot_hi = j % kMapFlush;
+      if (slot_hi == kMapFlush - 1 || j + 1 == n_vt) {
+        const int j0 = j - slot_hi;
+        const int hb = ((j / kMapFlush) & 1) * kMapFlush;
+        if (p.map_block == 64) {
+          if (tid < 2 * kMapFlush) {
+            const int qsub = tid / kMapFlush;
+            const int sl = tid % kMapFlush;
+            const int qblk = vrow_tile / 64 + qsub;
+            if (sl <= slot_hi && qblk >= 0 && qblk < p.map_nblk) {
+              const int c = cnt[(2 * qsub) * 2 * kMapFlush + hb + sl] +
+                            cnt[(2 * qsub + 1) * 2 * kMapFlush + hb + sl];
+              out_bh[static_cast<int64_t>(qblk) * p.map_nblk + j0 + sl] =
+                  Fp16::from_float(static_cast<float>(c) * inv_area);
+            }
+          }
+        } else {
+          if (tid < kMapFlush / 2) {
+            const int sl = tid;
+            const int qblk = vrow_tile / 128;
+            if (2 * sl + 1 <= slot_hi && qblk < p.map_nblk) {
+              int c = 0;
+#pragma unroll
+              for (int w = 0; w < 4; ++w)
+                c += cnt[w * 2 * kMapFlush + hb + 2 * sl] + cnt[w * 2 * kMapFlush + hb + 2 * sl + 1];
+              out_bh[static_cast<int64_t>(qblk) * p.map_nblk + j0 / 2 + sl] =
+                  Fp16::from_float(static_cast<float>(c) * inv_area);
+            }
+          }
+        }
+      }
+    }
+  }
 }
 
-template <int D, typename E, bool kSparse, bool kRagged>
+template <int D, typename E, bool kSparse, bool kRagged, bool kMap = false>
 int launch_attention_impl(const AttnParams& p, int batch, hipStream_t stream) {
   using L = AttnLds<D>;
-  auto kernel = attention_fwd_kernel<D, E, kSparse, kRagged>;
+  auto kernel = attention_fwd_kernel<D, E, kSparse, kRagged, kMap>;
+  constexpr int kLds = L::kTotal + (kMap ? kMapCountBytes : 0);
   static bool configured = false;  // the attribute is per function, same on every device
   if (!configured) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, L::kTotal) != hipSuccess) {
-      set_error("attention: cannot reserve %d bytes of LDS", L::kTotal);
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kLds) != hipSuccess) {
+      set_error("attention: cannot reserve %d bytes of LDS", kLds);
       return MODDIT_EHIP;
     }
     configured = true;
@@ -440,14 +573,16 @@ int launch_attention_impl(const AttnParams& p, int batch, hipStream_t stream) {
     set_error("attention: too many tiles (%lld)", static_cast<long long>(tiles));
     return MODDIT_EINVAL;
   }
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), L::kTotal,
-                     stream, p);
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), kLds, stream, p);
   MODDIT_CHECK_LAUNCH("attention");
   return MODDIT_OK;
 }
 
 template <int D, typename E, bool kSparse>
 int launch_attention(const AttnParams& p, int batch, hipStream_t stream) {
+  // The fused map pass addresses video key tiles that may extend past the last key
+  // (partial last block): always the range-checked path.
+  if (p.map != nullptr) return launch_attention_impl<D, E, false, true, true>(p, batch, stream);
   // Key counts that are a multiple of the tile (on an unshifted grid) need no clamping
   // or masking at all.
   if (p.kv_len % kBN == 0 && p.origin == 0)
@@ -455,11 +590,19 @@ int launch_attention(const AttnParams& p, int batch, hipStream_t stream) {
   return launch_attention_impl<D, E, kSparse, true>(p, batch, stream);
 }
 
+struct MapArgs {
+  void* out;
+  int q_off;
+  int video_blocks;
+  int block;
+  float log_thr;
+};
+
 int attention_entry(const void* q, const void* k, const void* v, void* o, float* lse, int batch,
                     int heads, int q_len, int kv_len, int head_dim, const int64_t* qs,
                     const int64_t* ks, const int64_t* vs, const int64_t* os, float scale,
                     int dtype, const int32_t* counts, const int32_t* entries, int n_qtiles,
-                    int cap, int origin, moddit_stream_t stream) {
+                    int cap, int origin, moddit_stream_t stream, const MapArgs* map = nullptr) {
   clear_error();
   MODDIT_CHECK_ARG(q && k && v && o, "attention: null tensor pointer");
   MODDIT_CHECK_ARG(qs && ks && vs && os, "attention: null stride array");
@@ -481,7 +624,8 @@ int attention_entry(const void* q, const void* k, const void* v, void* o, float*
     for (int j = 0; j < 3; ++j)
       MODDIT_CHECK_ARG(all[t][j] >= 0 && all[t][j] % 8 == 0,
                        "attention: strides must be non-negative multiples of 8 elements");
-  MODDIT_CHECK_ARG(origin > -kBN && origin <= 0,
+  // the fused map pass aligns the grid to 128-row tiles itself
+  MODDIT_CHECK_ARG(origin > (map ? -kBM : -kBN) && origin <= 0,
                    "attention: grid_origin must be in (-64, 0], got %d", origin);
   const bool sparse = counts != nullptr;
   const int nq = (q_len - origin + kBM - 1) / kBM;
@@ -529,6 +673,24 @@ int attention_entry(const void* q, const void* k, const void* v, void* o, float*
   }
   p.k_bytes = static_cast<uint32_t>(k_span);
   p.v_bytes = static_cast<uint32_t>(v_span);
+  p.map = nullptr;
+  if (map != nullptr) {
+    const int vt = map->video_blocks * map->block;
+    p.map = static_cast<uint16_t*>(map->out);
+    p.map_q_off = map->q_off;
+    p.map_kt0 = (map->q_off - origin) / kBN;
+    p.map_nblk = map->video_blocks;
+    p.map_block = map->block;
+    p.map_valid = vt < q_len - map->q_off ? vt : q_len - map->q_off;
+    p.map_scale = scale;
+    p.map_log_thr = map->log_thr;
+    // largest byte offset a video key tile forms
+    const int64_t map_off = (static_cast<int64_t>(map->q_off) - origin + vt) * ks[2] * 2;
+    if (map_off > 0x7fffffffLL) {
+      set_error("flash_fwd_map: one head's K span exceeds 2 GiB of 32-bit offsets");
+      return MODDIT_EUNSUPPORTED;
+    }
+  }
 
   hipStream_t st = as_stream(stream);
   const bool bf = dtype == MODDIT_BF16;
@@ -555,6 +717,32 @@ extern "C" int moddit_flash_fwd(const void* q, const void* k, const void* v, voi
   return moddit::attention_entry(q, k, v, o, lse, batch, heads, q_len, kv_len, head_dim,
                                  q_strides, k_strides, v_strides, o_strides, softmax_scale, dtype,
                                  nullptr, nullptr, 0, 0, 0, stream);
+}
+
+extern "C" int moddit_flash_fwd_map(const void* q, const void* k, const void* v, void* o,
+                                    float* lse, void* map_out, int batch, int heads, int seq_len,
+                                    int head_dim, const int64_t q_strides[3],
+                                    const int64_t k_strides[3], const int64_t v_strides[3],
+                                    const int64_t o_strides[3], float softmax_scale,
+                                    float log_threshold, int video_offset, int video_blocks,
+                                    int block_size, int dtype, moddit_stream_t stream) {
+  using namespace moddit;
+  clear_error();
+  MODDIT_CHECK_ARG(map_out != nullptr, "flash_fwd_map: map_out must not be NULL");
+  MODDIT_CHECK_ARG(block_size == 64 || block_size == 128,
+                   "flash_fwd_map: block_size must be 64 or 128, got %d", block_size);
+  MODDIT_CHECK_ARG(video_blocks > 0, "flash_fwd_map: video_blocks must be positive");
+  MODDIT_CHECK_ARG(video_offset >= 0, "flash_fwd_map: video offset must be non-negative");
+  // the last block may be partial, but must hold at least one token
+  MODDIT_CHECK_ARG(static_cast<int64_t>(video_offset) + static_cast<int64_t>(video_blocks - 1) * block_size < seq_len,
+                   "flash_fwd_map: video region exceeds sequence length");
+  MODDIT_CHECK_ARG(!std::isnan(log_threshold), "flash_fwd_map: NaN threshold");
+  // grid shifted so that video row 0 starts a 128-row tile
+  const int origin = video_offset - ((video_offset + kBM - 1) / kBM) * kBM;
+  MapArgs m{map_out, video_offset, video_blocks, block_size, log_threshold};
+  return attention_entry(q, k, v, o, lse, batch, heads, seq_len, seq_len, head_dim, q_strides,
+                         k_strides, v_strides, o_strides, softmax_scale, dtype, nullptr, nullptr,
+                         0, 0, origin, stream, &m);
 }
 
 extern "C" int moddit_block_sparse_fwd(const void* q, const void* k, const void* v, void* o,

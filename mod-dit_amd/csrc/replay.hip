@@ -22,13 +22,13 @@ namespace {
 constexpr int kBM = 128;
 constexpr int kBN = 64;
 constexpr int kThreads = 256;
-constexpr int kFlush = 64;  // key tiles per LDS count ring
+constexpr int kFlush = 64;  // key tiles per flush; the LDS count ring holds two flushes
 
 template <int D>
 struct ReplayLds {
   static constexpr int kPitchK = D * 2 + 16;
   static constexpr int kKBytes = kBN * kPitchK;
-  static constexpr int kCounts = 4 * kFlush * 4;  // int per (wave, ring slot)
+  static constexpr int kCounts = 4 * 2 * kFlush * 4;  // int per (wave, ring slot)
   static constexpr int kTotal = 2 * kKBytes + kCounts;
 };
 
@@ -177,7 +177,9 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
           total += __builtin_popcountll(__ballot(s1[i] < thr));
         }
       }
-      if (lane == 0) cnt[wave * kFlush + (it % kFlush)] = total;
+      // two halves of kFlush slots: a flush reads one half while the next kFlush key
+      // tiles (at least one barrier later) write the other
+      if (lane == 0) cnt[wave * 2 * kFlush + (it % (2 * kFlush))] = total;
     }
 
     if (has_next) store_tile((it + 1) & 1);
@@ -185,7 +187,8 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
 
     const int slot_hi = it % kFlush;
     if (slot_hi == kFlush - 1 || !has_next) {
-      const int it0 = it - slot_hi;  // first key tile of this ring
+      const int it0 = it - slot_hi;  // first key tile of this flush
+      const int hb = ((it / kFlush) & 1) * kFlush;  // ring half it was written to
       if (p.block == 64) {
         // two 64-row query blocks per tile; one key block per key tile
         if (tid < 2 * kFlush) {
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
           const int s = tid % kFlush;
           const int qblk = 2 * qt + qsub;
           if (s <= slot_hi && qblk < p.nblk) {
-            const int c = cnt[(2 * qsub) * kFlush + s] + cnt[(2 * qsub + 1) * kFlush + s];
+            const int c = cnt[(2 * qsub) * 2 * kFlush + hb + s] + cnt[(2 * qsub + 1) * 2 * kFlush + hb + s];
             const float ratio = static_cast<float>(c) * inv_area;
             out_bh[static_cast<int64_t>(qblk) * p.nblk + it0 + s] = Fp16::from_float(ratio);
           }
@@ -205,7 +208,8 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
           if (2 * s + 1 <= slot_hi) {
             int c = 0;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) c += cnt[w * kFlush + 2 * s] + cnt[w * kFlush + 2 * s + 1];
+            for (int w = 0; w < 4; ++w)
+              c += cnt[w * 2 * kFlush + hb + 2 * s] + cnt[w * 2 * kFlush + hb + 2 * s + 1];
             const float ratio = static_cast<float>(c) * inv_area;
             out_bh[static_cast<int64_t>(qt) * p.nblk + it0 / 2 + s] = Fp16::from_float(ratio);
           }

@@ -7,6 +7,10 @@ Drop-in for MoD/mod/triton_flash_sparsity.py (public entry `flash_attn_with_spar
   pass 2  replay of the video x video QK tiles, counting probabilities below the
           threshold: count(bf16(q*scale).k < lse + ln(threshold)) / block_size^2 -> fp16
 
+Two kernels on purpose: the single-kernel form (`ops.flash_fwd_map`, same results) runs
+its replay sweep at the attention kernel's occupancy (two waves per SIMD) and is slower
+on gfx950 than the standalone replay kernel at four.
+
 There is a single backend (gfx950 HIP); the reference's Triton fallback and its
 MOD_DIT_SPARSITY_BACKEND switch have no counterpart here.
 """

@@ -123,6 +123,34 @@ def block_sparse_fwd(q, k, v, tiles: TileList, softmax_scale=None, return_lse=Fa
     return _attention(q, k, v, softmax_scale, return_lse, tiles, out)
 
 
+def flash_fwd_map(q, k, v, *, softmax_scale, log_threshold, video_offset, video_blocks,
+                  block_size, return_lse=True, out=None):
+    """Dense self-attention and the fp16 (B,H,n,n) sparsity map in one kernel.
+
+    Returns (O, LSE or None, map). The map equals `sparsity_map` applied to this LSE."""
+    _require_gpu(q, k, v, what="flash_fwd_map")
+    if q.ndim != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("query, key and value must have identical shape [B, H, S, D]")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("query, key, and value must have the same dtype")
+    dt = _attn_dtype(q)
+    B, H, S, D = q.shape
+    if D not in (64, 128):
+        raise ValueError(f"head_dim must be 64 or 128, got {D}")
+    q, k, v = _attn_view(q), _attn_view(k), _attn_view(v)
+    if out is None:
+        out = torch.empty((B, H, S, D), device=q.device, dtype=q.dtype)
+    lse = torch.empty((B, H, S), device=q.device, dtype=torch.float32) if return_lse else None
+    smap = torch.empty((B, H, video_blocks, video_blocks), device=q.device, dtype=torch.float16)
+    check(_lib.load().moddit_flash_fwd_map(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), _ptr(lse), smap.data_ptr(),
+        B, H, S, D, strides3(*q.stride()[:3]), strides3(*k.stride()[:3]),
+        strides3(*v.stride()[:3]), strides3(*out.stride()[:3]), float(softmax_scale),
+        float(log_threshold), int(video_offset), int(video_blocks), int(block_size), dt,
+        _stream(q)), "moddit_flash_fwd_map")
+    return out, lse, smap
+
+
 # --------------------------------------------------------------------------------------
 # sparsity map replay
 # --------------------------------------------------------------------------------------

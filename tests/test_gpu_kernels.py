@@ -158,6 +158,20 @@ def test_block_sparse_shifted_grid_matches_masked_fp64(text, video, D, union):
     np.testing.assert_allclose(_np(lse[0]), ref_lse, rtol=0, atol=2e-3)
 
 
+def test_attention_kernels_are_deterministic():
+    """Repeated calls give identical bits (regression: the tile DMA is inline asm, so the
+    wait states after m0 / descriptor writes are the asm's job; a missing one showed as
+    run-to-run differences)."""
+    H, S, D, bs = 8, 8192, 128, 64
+    q, k, v = (_randn((1, H, S, D), 700 + i, torch.bfloat16) for i in range(3))
+    m = _random_block_mask(H, S // bs, 0.2, 31)
+    tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=False)
+    runs = [(ops.flash_fwd(q, k, v), ops.block_sparse_fwd(q, k, v, tiles)) for _ in range(3)]
+    for (d, sp) in runs[1:]:
+        assert torch.equal(d[0], runs[0][0][0]) and torch.equal(d[1], runs[0][0][1])
+        assert torch.equal(sp[0], runs[0][1][0])
+
+
 # ====================================================================== sparsity map
 def _layout(model_type, bs):
     # tests/test_flash_sparsity.py:22-25
@@ -219,6 +233,50 @@ def test_sparsity_map_partial_last_block_dyadic_bit_exact(text, video, bs, D, dt
     ref = O.replay_map(qn[0], kn[0], lse[0], scale=scale, log_threshold=ln_thr, q_off=qo,
                        k_off=ko, video_blocks=vb, block_size=bs, dtype=dt)
     assert np.array_equal(got[0].cpu().numpy(), ref), (text, video, bs, D, dtype)
+
+
+@pytest.mark.parametrize("model_type,video,text,bs,D,dtype", [
+    ("wan", 1024, 0, 64, 128, torch.bfloat16),
+    ("hunyuan", 1024, 256, 128, 64, torch.float16),
+    ("cogvideox", 450, 50, 64, 64, torch.bfloat16),    # partial last block, shifted grid
+    ("cogvideox", 400, 130, 128, 128, torch.bfloat16),  # 128-blocks, grid origin -126
+])
+def test_flash_fwd_map_fused_pass(model_type, video, text, bs, D, dtype):
+    """Dense pass + map in one kernel: the map is bit-exact to the replay of the kernel's
+    own LSE (oracle and the separate replay kernel), O/LSE match the dense kernel."""
+    S = video + text
+    rng = np.random.default_rng(S + bs + D)
+    qn = rng.integers(-4, 5, size=(1, 2, S, D)).astype(np.float32) / 8
+    kn = rng.integers(-4, 5, size=(1, 2, S, D)).astype(np.float32) / 8
+    q = torch.from_numpy(qn).to(dtype).to(DEV)
+    k = torch.from_numpy(kn).to(dtype).to(DEV)
+    v = _randn((1, 2, S, D), 900, dtype)
+    scale = D ** -0.5
+    vb, qo, _ = O.video_layout(model_type, S, video, text, bs)
+    ln_thr = math.log(1e-2)
+    out, lse, smap = ops.flash_fwd_map(q, k, v, softmax_scale=scale, log_threshold=ln_thr,
+                                       video_offset=qo, video_blocks=vb, block_size=bs)
+    assert smap.shape == (1, 2, vb, vb) and smap.dtype == torch.float16
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    ref = O.replay_map(qn[0], kn[0], _np(lse[0]), scale=scale, log_threshold=ln_thr, q_off=qo,
+                       k_off=qo, video_blocks=vb, block_size=bs, dtype=dt)
+    assert np.array_equal(smap[0].cpu().numpy(), ref)
+    sep = md.cuda_sparsity_map(q, k, lse, softmax_scale=scale, log_threshold=ln_thr,
+                               q_video_offset=qo, k_video_offset=qo, video_blocks=vb, block_size=bs)
+    assert torch.equal(sep, smap)
+    # the dense pass is the dense kernel's algorithm in its range-checked instantiation
+    # (FMA contraction may differ, so P can round differently): close to it, and
+    # deterministic across calls
+    o2, lse2 = ops.flash_fwd(q, k, v)
+    assert (out.float() - o2.float()).abs().max().item() <= 4e-3
+    if qo % 128 == 0:
+        assert (lse - lse2).abs().max().item() <= 1e-5
+    out3, lse3, smap3 = ops.flash_fwd_map(q, k, v, softmax_scale=scale, log_threshold=ln_thr,
+                                          video_offset=qo, video_blocks=vb, block_size=bs)
+    assert torch.equal(out3, out) and torch.equal(lse3, lse) and torch.equal(smap3, smap)
+    ref_o, ref_lse = O.masked_attention(qn[0], kn[0], _np(v[0]), None, dtype=np.float64)
+    _check_attn(out[0], ref_o, f"fused dense {model_type} bs={bs}")
+    np.testing.assert_allclose(_np(lse[0]), ref_lse, rtol=0, atol=2e-3)
 
 
 @pytest.mark.parametrize("bs", [64, 128])
