@@ -12,7 +12,10 @@ One step = one block-sparse attention call over the whole layer with the predict
 (dense-equivalent, 4*H*N^2*d) TFLOP/s of that call; executed TFLOP/s, the dense
 baseline, the mask-prediction overhead and the CPU baseline are reported beside it.
 
-    python bench.py [--steps K] [--warmup W] [--tile-rows union|exact] [--no-cpu]
+The int8/fp8 path (quantiser + int8 Q.K^T / fp8 P.V kernels) is timed on the same layer
+and tiles and reported under "q8" (a reported alternative; the headline stays bf16).
+
+    python bench.py [--steps K] [--warmup W] [--tile-rows union|exact] [--no-cpu] [--no-q8]
 """
 from __future__ import annotations
 
@@ -337,6 +340,33 @@ def cpu_baseline(q, k, v, tiles, budget_s=12.0):
 
 
 # ------------------------------------------------------------------------------------
+def q8_leg(q, k, v, tiles, out, *, ref, eff_flop, reps):
+    """Timings of the int8/fp8 path on the same layer and tiles: quantiser, block-sparse and
+    dense kernels (HIP events on the launch stream), and the error of its output against
+    the bf16 kernel's (`ref`)."""
+    qz = ops.quantize_qkv(q, k, v)
+    ops.block_sparse_fwd_q8(qz, tiles, out=out)
+    torch.cuda.synchronize()
+    diff = (out.float() - ref.float()).abs()
+    err_max, err_mean = float(diff.max()), float(diff.mean())
+    del diff
+    quant = time_events(lambda: ops.quantize_qkv(q, k, v), 3)
+    sp = time_events(lambda: ops.block_sparse_fwd_q8(qz, tiles, out=out), max(3, reps // 2))
+    dn = time_events(lambda: ops.flash_fwd_q8(qz, return_lse=False, out=out), 2)
+    quant_ms, sparse_ms, dense_ms = min(quant), sum(sp) / len(sp), min(dn)
+    return {
+        "dtype": "int8 Q.K^T, fp8 e4m3 P.V, fp32 softmax",
+        "quantize_ms": round(quant_ms, 3),
+        "sparse_ms": round(sparse_ms, 3),
+        "sparse_eff_tflops": round(eff_flop / (sparse_ms * 1e-3) / 1e12, 3),
+        "sparse_incl_quantize_ms": round(sparse_ms + quant_ms, 3),
+        "dense_ms": round(dense_ms, 3),
+        "dense_tflops": round(eff_flop / (dense_ms * 1e-3) / 1e12, 3),
+        "vs_bf16_sparse_max_abs": round(err_max, 5),
+        "vs_bf16_sparse_mean_abs": round(err_mean, 6),
+    }
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -347,10 +377,12 @@ def main(argv=None):
     ap.add_argument("--threshold", type=float, default=1e-4)
     ap.add_argument("--dense-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-q8", action="store_true", help="skip the int8/fp8 path's timings")
     ap.add_argument("--sweep", action="store_true",
                     help="configs[4]: 50-step denoising trajectory (W=12, T=10) with sparsity "
                          "ramping 50%%->90%%; prints its own JSON line")
-    ap.add_argument("--profile", choices=("sparse", "dense", "replay", "mask", "copy"), default=None,
+    ap.add_argument("--profile", choices=("sparse", "dense", "replay", "mask", "copy", "q8"),
+                    default=None,
                     help="run only the named kernel(s) after setup (for rocprofv3 counter passes); "
                          "prints no JSON")
     args = ap.parse_args(argv)
@@ -421,6 +453,8 @@ def main(argv=None):
                                  k_video_offset=0, video_blocks=N // bs, block_size=bs)
             elif args.profile == "mask":
                 mask_overhead_once(art, bpf=bpf, block_size=bs, union=union)
+            elif args.profile == "q8":
+                ops.block_sparse_fwd_q8(ops.quantize_qkv(q, k, v), tiles, out=out)
         torch.cuda.synchronize()
         log(f"profile {args.profile}: {args.steps} calls done")
         return 0
@@ -466,6 +500,11 @@ def main(argv=None):
                                                block_size=bs, return_lse=False,
                                                out=dense_out), 2)
     map_step_fused_ms = min(fm)
+
+    q8 = None
+    if not args.no_q8:
+        log("timing the int8/fp8 path")
+        q8 = q8_leg(q, k, v, tiles, out, ref=out.clone(), eff_flop=eff_flop, reps=args.steps)
 
     cpu = None
     if not args.no_cpu:
@@ -520,6 +559,7 @@ def main(argv=None):
             "kernel_ms": round(kernel_ms, 4),
         },
         "cpu_baseline": cpu,
+        "q8": q8,
         "host": {"cpu_count": os.cpu_count(), "machine": platform.processor() or platform.machine(),
                  "torch": torch.__version__},
     }

@@ -109,6 +109,59 @@ int moddit_flash_fwd_map(const void* q, const void* k, const void* v, void* o, f
                          int video_blocks, int block_size, int dtype, moddit_stream_t stream);
 
 /*
+ * Quantisation pass of the int8/fp8 attention path (SageAttention2-style: int8 Q.K^T,
+ * fp8 e4m3 P.V), for self-attention q/k/v of shape (B,H,S,D), D in {64,128}.
+ * Blocks and tiles lie on the attention grid that starts at token grid_origin (-63..0, the
+ * grid_origin later given to moddit_block_sparse_fwd_q8; 0 for the dense kernel): grid
+ * position c is token grid_origin + c, tokens outside [0,S) count as zero, G = S - grid_origin.
+ *   q8[bh][s][d]  = rne(q * 127/amax_q), amax_q over each 32-position block of the grid
+ *   k8[bh][s][d]  = rne((k - k_mean[bh][d]) * 127/amax_k), amax_k over each 64-position
+ *                   tile, k_mean = per-channel mean over the sequence
+ *   v8t[bh][d][c] = e4m3_rne(v[grid_origin + c] * 448/amax_v[d]), amax_v per channel over
+ *                   the sequence; grid positions contiguous, s_pad = ceil(G/64)*64 columns,
+ *                   zero outside the sequence
+ *   q_scale [bh][ceil(G/32)] = amax_q/127, k_scale [bh][ceil(G/64)] = amax_k/127,
+ *   v_scale [bh][D] = amax_v/448 (each 1 where the amax is 0), k_mean [bh][D],
+ *   q_kmean [bh][S] = q . k_mean in fp32 (the attention kernels add softmax_scale times it
+ *                     to the LSE, which then is that of the unsmoothed scores).
+ * workspace: moddit_quantize_workspace_floats(B,H,D) floats (deterministic partial
+ * column statistics; contents are scratch). All buffers are caller-allocated.
+ * No counterpart call in the reference: its quantised engine, block_sparse_sage2_attn_cuda
+ * (MoD/mod/attn_mask.py:306), quantises internally (third-party, not in the tree).
+ */
+int moddit_quantize_qkv(const void* q, const void* k, const void* v, int batch, int heads,
+                        int seq_len, int head_dim, const int64_t q_strides[3],
+                        const int64_t k_strides[3], const int64_t v_strides[3], int dtype,
+                        int grid_origin, float* workspace, int8_t* q8, float* q_scale,
+                        int8_t* k8, float* k_scale, uint8_t* v8t, float* v_scale,
+                        float* k_mean, float* q_kmean, moddit_stream_t stream);
+int moddit_quantize_workspace_floats(int batch, int heads, int head_dim);
+
+/*
+ * Attention on the output of moddit_quantize_qkv: scores from the int8 product times
+ * q_scale * k_scale, fp32 online softmax, P rounded to e4m3 for the fp8 P.V product,
+ * O = (P.V8) * v_scale[d] / rowsum written as dtype (bf16/fp16) with the given strides,
+ * natural-log LSE (may be NULL; needs q_kmean when not). moddit_block_sparse_fwd_q8 takes
+ * the tile lists and grid origin of moddit_block_sparse_fwd; the quantisation must have
+ * used the same grid_origin (the dense kernel: 0).
+ * Replaces block_sparse_sage2_attn_cuda (MoD/mod/attn_mask.py:306,312-317) and sageattn
+ * (attn_mask.py:271-276) with their own quantised arithmetic (parity unpinned against
+ * them; pinned against exact attention on the dequantised inputs).
+ */
+int moddit_flash_fwd_q8(const int8_t* q8, const float* q_scale, const int8_t* k8,
+                        const float* k_scale, const uint8_t* v8t, const float* v_scale,
+                        const float* q_kmean, void* o, float* lse, int batch, int heads,
+                        int seq_len, int head_dim, const int64_t o_strides[3],
+                        float softmax_scale, int dtype, moddit_stream_t stream);
+int moddit_block_sparse_fwd_q8(const int8_t* q8, const float* q_scale, const int8_t* k8,
+                               const float* k_scale, const uint8_t* v8t, const float* v_scale,
+                               const float* q_kmean, void* o, float* lse, int batch, int heads,
+                               int seq_len, int head_dim, const int64_t o_strides[3],
+                               float softmax_scale, int dtype, const int32_t* counts,
+                               const int32_t* entries, int n_qtiles, int cap, int grid_origin,
+                               moddit_stream_t stream);
+
+/*
  * Replayed block sparsity map (video x video blocks), fp16 output (B,H,n,n):
  *   map[b,h,i,j] = fp16_rn( #{(r,c) in block (i,j) :
  *                   fp32(sum_d round(q[r,d]*scale) * k[c,d]) < lse[r] + log_threshold}

@@ -37,6 +37,13 @@ _SIGNATURES = {
     "moddit_flash_fwd_map": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                                   _c_i64p, _c_i64p, _c_i64p, _c_i64p, _f, _f, _i, _i, _i, _i,
                                   _vp]),
+    "moddit_quantize_qkv": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _c_i64p, _c_i64p, _c_i64p, _i,
+                                 _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "moddit_quantize_workspace_floats": (_i, [_i, _i, _i]),
+    "moddit_flash_fwd_q8": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
+                                 _c_i64p, _f, _i, _vp]),
+    "moddit_block_sparse_fwd_q8": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i,
+                                        _i, _c_i64p, _f, _i, _vp, _vp, _i, _i, _i, _vp]),
     "moddit_sparsity_map": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _c_i64p, _c_i64p,
                                  _f, _f, _i, _i, _i, _i, _i, _vp]),
     "moddit_mts": (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),

@@ -152,6 +152,109 @@ def flash_fwd_map(q, k, v, *, softmax_scale, log_threshold, video_offset, video_
 
 
 # --------------------------------------------------------------------------------------
+# int8 / fp8 attention (SageAttention2-style quantised engine)
+# --------------------------------------------------------------------------------------
+@dataclass
+class QuantizedQKV:
+    """Output of `quantize_qkv` (all on the device; see include/moddit.h)."""
+
+    q8: torch.Tensor       # int8 (B,H,S,D)
+    q_scale: torch.Tensor  # fp32 (B,H,ceil(G/32)), G = S - origin: 32-position grid blocks
+    k8: torch.Tensor       # int8 (B,H,S,D), K minus its per-channel mean
+    k_scale: torch.Tensor  # fp32 (B,H,ceil(G/64)): 64-position grid tiles
+    v8t: torch.Tensor      # uint8 e4m3 (B,H,D,s_pad), column c = token origin + c
+    v_scale: torch.Tensor  # fp32 (B,H,D)
+    k_mean: torch.Tensor   # fp32 (B,H,D)
+    q_kmean: torch.Tensor  # fp32 (B,H,S): q . k_mean, the LSE correction
+    dtype: torch.dtype     # of the source tensors (and of the attention output)
+    origin: int = 0        # first token of the attention grid the blocks lie on
+
+    @property
+    def shape(self):
+        return tuple(self.q8.shape)
+
+
+def quantize_qkv(q, k, v, grid_origin: int = 0) -> QuantizedQKV:
+    """Quantise self-attention q/k/v (B,H,S,D) bf16/fp16 for the int8/fp8 kernels, with
+    blocks on the attention grid that starts at token `grid_origin` (-63..0: the
+    `TileList.origin` the block-sparse kernel will run on; 0 for dense attention)."""
+    _require_gpu(q, k, v, what="quantize_qkv")
+    if q.ndim != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("query, key and value must have identical shape [B, H, S, D]")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("query, key, and value must have the same dtype")
+    dt = _attn_dtype(q)
+    B, H, S, D = q.shape
+    if D not in (64, 128):
+        raise ValueError(f"head_dim must be 64 or 128, got {D}")
+    if not -64 < grid_origin <= 0:
+        raise ValueError(f"grid_origin must lie in (-64, 0], got {grid_origin}")
+    q, k, v = _attn_view(q), _attn_view(k), _attn_view(v)
+    dev = q.device
+    G = S - grid_origin
+    s_pad = (G + 63) // 64 * 64
+    lib = _lib.load()
+    ws = torch.empty(lib.moddit_quantize_workspace_floats(B, H, D), device=dev, dtype=torch.float32)
+    out = QuantizedQKV(
+        q8=torch.empty((B, H, S, D), device=dev, dtype=torch.int8),
+        q_scale=torch.empty((B, H, (G + 31) // 32), device=dev, dtype=torch.float32),
+        k8=torch.empty((B, H, S, D), device=dev, dtype=torch.int8),
+        k_scale=torch.empty((B, H, s_pad // 64), device=dev, dtype=torch.float32),
+        v8t=torch.empty((B, H, D, s_pad), device=dev, dtype=torch.uint8),
+        v_scale=torch.empty((B, H, D), device=dev, dtype=torch.float32),
+        k_mean=torch.empty((B, H, D), device=dev, dtype=torch.float32),
+        q_kmean=torch.empty((B, H, S), device=dev, dtype=torch.float32),
+        dtype=q.dtype, origin=int(grid_origin))
+    check(lib.moddit_quantize_qkv(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), B, H, S, D, strides3(*q.stride()[:3]),
+        strides3(*k.stride()[:3]), strides3(*v.stride()[:3]), dt, int(grid_origin),
+        ws.data_ptr(), out.q8.data_ptr(), out.q_scale.data_ptr(), out.k8.data_ptr(),
+        out.k_scale.data_ptr(), out.v8t.data_ptr(), out.v_scale.data_ptr(),
+        out.k_mean.data_ptr(), out.q_kmean.data_ptr(), _stream(q)),
+        "moddit_quantize_qkv")
+    return out
+
+
+def _attention_q8(qz: QuantizedQKV, scale, return_lse, tiles: TileList | None, out=None):
+    B, H, S, D = qz.shape
+    if out is None:
+        out = torch.empty((B, H, S, D), device=qz.q8.device, dtype=qz.dtype)
+    lse = torch.empty((B, H, S), device=out.device, dtype=torch.float32) if return_lse else None
+    if scale is None:
+        scale = D ** -0.5
+    dt = _attn_dtype(out)
+    lib = _lib.load()
+    origin = 0 if tiles is None else int(tiles.origin)
+    if qz.origin != origin:
+        raise ValueError(f"q/k/v were quantised on the grid starting at {qz.origin}, the "
+                         f"attention runs on the grid starting at {origin}")
+    args = (qz.q8.data_ptr(), qz.q_scale.data_ptr(), qz.k8.data_ptr(), qz.k_scale.data_ptr(),
+            qz.v8t.data_ptr(), qz.v_scale.data_ptr(), qz.q_kmean.data_ptr(), out.data_ptr(),
+            _ptr(lse), B, H, S, D, strides3(*out.stride()[:3]), float(scale), dt)
+    if tiles is None:
+        check(lib.moddit_flash_fwd_q8(*args, _stream(out)), "moddit_flash_fwd_q8")
+    else:
+        if tiles.counts.shape[0] != H:
+            raise ValueError(f"tile lists cover {tiles.counts.shape[0]} heads, attention has {H}")
+        check(lib.moddit_block_sparse_fwd_q8(*args, tiles.counts.data_ptr(),
+                                             tiles.entries.data_ptr(), tiles.n_qtiles, tiles.cap,
+                                             int(tiles.origin), _stream(out)),
+              "moddit_block_sparse_fwd_q8")
+    return out, lse
+
+
+def flash_fwd_q8(qz: QuantizedQKV, softmax_scale=None, return_lse=True, out=None):
+    """Dense int8/fp8 attention on quantised q/k/v; returns (O, LSE or None)."""
+    return _attention_q8(qz, softmax_scale, return_lse, None, out)
+
+
+def block_sparse_fwd_q8(qz: QuantizedQKV, tiles: TileList, softmax_scale=None, return_lse=False,
+                        out=None):
+    """Block-sparse int8/fp8 attention over the active key tiles of `tiles`."""
+    return _attention_q8(qz, softmax_scale, return_lse, tiles, out)
+
+
+# --------------------------------------------------------------------------------------
 # sparsity map replay
 # --------------------------------------------------------------------------------------
 def sparsity_map(query, key, lse, *, softmax_scale, log_threshold, q_video_offset,

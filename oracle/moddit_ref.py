@@ -16,7 +16,7 @@ __all__ = [
     "choose_topk_lines", "generate_mask_from_lines", "mask_cell", "tiles_from_mask",
     "token_mask_from_tiles", "token_mask_from_blocks", "masked_attention",
     "probability_map", "replay_map", "refresh_merge", "step_phase", "video_layout",
-    "cogvideox_grid",
+    "cogvideox_grid", "e4m3_decode", "e4m3_encode", "quantize_qkv", "attention_q8",
     "MODE_SPARSE", "MODE_BLOCK_DIAGONAL", "MODE_FULL",
 ]
 
@@ -478,6 +478,153 @@ def replay_map(q, k, lse, *, scale: float, log_threshold: float, q_off: int, k_o
         cnt = below.reshape(video_blocks, block_size, video_blocks, block_size).sum(axis=(1, 3))
         out[h] = (cnt.astype(np.float32) / np.float32(block_size * block_size)).astype(np.float16)
     return out
+
+
+# --------------------------------------------------------------------------------------
+# int8 / fp8 attention (the quantised engine, block_sparse_sage2_attn_cuda at
+# MoD/mod/attn_mask.py:306, restated as SageAttention2's published scheme: int8 Q.K^T
+# with per-block scales on a mean-smoothed K, fp8 e4m3 P.V with per-channel V scales)
+# --------------------------------------------------------------------------------------
+def e4m3_decode(b: np.ndarray) -> np.ndarray:
+    """OCP FP8 E4M3 (bias 7, max 448, 0x7f/0xff NaN) bytes -> float64."""
+    b = np.asarray(b).astype(np.int64)
+    sign = np.where(b & 0x80, -1.0, 1.0)
+    e = (b >> 3) & 0xF
+    m = b & 7
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1 + m / 8.0) * 2.0 ** (e - 7))
+    mag = np.where((b & 0x7F) == 0x7F, np.nan, mag)
+    return sign * mag
+
+
+def e4m3_encode(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even float -> OCP E4M3 bytes (|x| <= 448)."""
+    x = np.asarray(x, dtype=np.float64)
+    table = e4m3_decode(np.arange(128))  # non-negative codes 0..127 (127 is NaN)
+    vals = table[:127]
+    a = np.abs(x)
+    idx = np.searchsorted(vals, a)  # vals[idx-1] < a <= vals[idx]
+    idx = np.clip(idx, 1, 126)
+    lo, hi = vals[idx - 1], vals[idx]
+    pick_hi = (a - lo > hi - a) | ((a - lo == hi - a) & (idx % 2 == 0))
+    code = np.where(pick_hi, idx, idx - 1)
+    code = np.where(a >= vals[126], 126, code)
+    code = np.where(a == 0, 0, code)
+    return (code | np.where(x < 0, 0x80, 0)).astype(np.uint8)
+
+
+def quantize_qkv(q, k, v, k_mean: Optional[np.ndarray] = None,
+                 origin: int = 0) -> Dict[str, np.ndarray]:
+    """Quantise one batch element's q/k/v (H, S, D) (values exact in fp32).
+
+    Follows the fp32 operations of the definition in include/moddit.h: blocks of 32 and
+    tiles of 64 positions on the grid that starts at token `origin` (tokens outside the
+    sequence count as zero), scale = amax/127 (or 448), x * (127/amax) rounded
+    half-to-even, K minus its per-channel mean (the mean is taken from `k_mean` when given,
+    so the rest can be compared bit for bit), v8t column c = token origin + c.
+    q_kmean = q . k_mean in fp64."""
+    f32 = np.float32
+    q = np.asarray(q, f32)
+    k = np.asarray(k, f32)
+    v = np.asarray(v, f32)
+    H, S, D = q.shape
+    if k_mean is None:
+        k_mean = (k.astype(np.float64).mean(axis=1)).astype(f32)
+    k_mean = np.asarray(k_mean, f32)
+    G = S - origin
+    nqb, nkt = (G + 31) // 32, (G + 63) // 64
+    s_pad = nkt * 64
+
+    def grid(x):  # (H, S, D) -> (H, s_pad, D) on the grid, zero outside the sequence
+        g = np.zeros((H, s_pad, D), f32)
+        g[:, -origin:-origin + S] = x
+        return g
+
+    out = dict(q8=np.zeros((H, S, D), np.int8), q_scale=np.zeros((H, nqb), f32),
+               k8=np.zeros((H, S, D), np.int8), k_scale=np.zeros((H, nkt), f32),
+               v8t=np.zeros((H, D, s_pad), np.uint8), v_scale=np.zeros((H, D), f32),
+               k_mean=k_mean,
+               q_kmean=np.einsum("hsd,hd->hs", q.astype(np.float64), k_mean.astype(np.float64)))
+
+    def q_int(x, amax):
+        inv = f32(127) / amax if amax > 0 else f32(1)
+        return np.clip(np.rint((x * inv).astype(f32)), -127, 127).astype(np.int8)
+
+    qg = grid(q)
+    kg = grid((k - k_mean[:, None, :]).astype(f32))
+    q8g = np.zeros((H, s_pad, D), np.int8)
+    k8g = np.zeros((H, s_pad, D), np.int8)
+    for h in range(H):
+        for b in range(nqb):
+            blk = qg[h, 32 * b:32 * b + 32]
+            am = f32(np.abs(blk).max())
+            q8g[h, 32 * b:32 * b + 32] = q_int(blk, am)
+            out["q_scale"][h, b] = am / f32(127) if am > 0 else f32(1)
+        for t in range(nkt):
+            blk = kg[h, 64 * t:64 * t + 64]
+            am = f32(np.abs(blk).max())
+            k8g[h, 64 * t:64 * t + 64] = q_int(blk, am)
+            out["k_scale"][h, t] = am / f32(127) if am > 0 else f32(1)
+        vam = np.abs(v[h]).max(axis=0).astype(f32)
+        vinv = np.where(vam > 0, f32(448) / np.where(vam > 0, vam, 1), f32(1)).astype(f32)
+        out["v_scale"][h] = np.where(vam > 0, vam / f32(448), f32(1))
+        out["v8t"][h, :, -origin:-origin + S] = e4m3_encode((v[h] * vinv[None, :]).astype(f32)).T
+    out["q8"] = q8g[:, -origin:-origin + S]
+    out["k8"] = k8g[:, -origin:-origin + S]
+    return out
+
+
+def attention_q8(qz: Dict[str, np.ndarray], token_mask: Optional[np.ndarray] = None,
+                 scale: Optional[float] = None, slack: float = 1.5, shift: float = 7.0,
+                 origin: int = 0):
+    """Attention on quantised inputs (the output of `quantize_qkv` with the same `origin`),
+    in fp64, modelling the kernel's arithmetic: scores int8.int8 * q_scale * k_scale (log2
+    units); key tiles of 64 on the grid starting at token `origin` visited in ascending
+    order, the row max moved only when a tile's max exceeds it by more than `slack`;
+    P = exp2(s - m + shift) rounded to e4m3 for the P.V product, the row sum over the
+    unrounded P, earlier tiles rescaled by 2^(m_old - m_new); O times v_scale.
+    LSE (natural log) = ln(sum P) + (m - shift) ln 2 + scale * q_kmean.
+    Returns (O (H, S, D), LSE (H, S)); rows without keys: O = 0, LSE = -inf."""
+    q8 = qz["q8"].astype(np.float64)
+    k8 = qz["k8"].astype(np.float64)
+    H, S, D = q8.shape
+    if scale is None:
+        scale = D ** -0.5
+    pos = np.arange(S) - origin  # grid position of each token
+    qs = qz["q_scale"].astype(np.float64)[:, pos // 32]
+    ks = qz["k_scale"].astype(np.float64)[:, pos // 64]
+    v = e4m3_decode(qz["v8t"][:, :, pos]).transpose(0, 2, 1)  # (H, S, D)
+    vs = qz["v_scale"].astype(np.float64)
+    out = np.zeros((H, S, D))
+    lse = np.full((H, S), -np.inf)
+    nt = (S - origin + 63) // 64
+    for h in range(H):
+        s_all = (q8[h] @ k8[h].T) * qs[h][:, None] * ks[h][None, :] * scale * np.log2(np.e)
+        if token_mask is not None:
+            s_all = np.where(token_mask[h], s_all, -np.inf)
+        m = np.full(S, -np.inf)
+        acc = np.zeros((S, D))
+        l = np.zeros(S)
+        for t in range(nt):
+            k0, k1 = max(origin + 64 * t, 0), min(origin + 64 * t + 64, S)
+            st = s_all[:, k0:k1]
+            mx = st.max(axis=1)
+            act = np.isfinite(mx)  # rows for which this tile holds a key
+            need = act & (mx > m + slack)
+            m_new = np.where(need, mx, m)
+            fin_new = np.where(np.isfinite(m_new), m_new, 0)
+            alpha = np.where(np.isfinite(m), np.exp2(np.where(np.isfinite(m), m - fin_new, 0)), 0.0)
+            alpha = np.where(act, np.where(need, alpha, 1.0), 1.0)
+            p = np.where(act[:, None], np.exp2(st - (fin_new - shift)[:, None]), 0.0)
+            p8 = e4m3_decode(e4m3_encode(p))
+            acc = acc * alpha[:, None] + p8 @ v[h, k0:k1]
+            l = l * alpha + p.sum(axis=1)
+            m = m_new
+        o = acc * vs[h][None, :]
+        ok = l > 0
+        out[h] = np.where(ok[:, None], o / np.where(ok, l, 1)[:, None], 0)
+        lse[h] = np.where(ok, np.log(np.where(ok, l, 1)) + (np.where(ok, m, 0) - shift) * np.log(2)
+                          + scale * qz["q_kmean"][h], -np.inf)
+    return out, lse
 
 
 def refresh_merge(prev: np.ndarray, cur: np.ndarray, mask: np.ndarray) -> np.ndarray:

@@ -1,0 +1,149 @@
+"""Parity of the int8/fp8 (SageAttention2-style) path with the CPU oracle (GPU only).
+
+- quantisation: bit-exact against the oracle's fp32 restatement (given the kernel's
+  per-channel K mean, itself checked against the fp64 mean), on the unshifted and on a
+  shifted grid, and deterministic; q . mean_k within fp32 summation error;
+- attention: against fp64 attention on the same quantised values with the kernel's tile
+  order and lazy row max modelled (max-abs <= 4e-3, mean-abs <= 2e-4: what remains is
+  exp2 rounding flipping an e4m3 rounding of P now and then, and fp32 accumulation), and
+  against exact attention on the unquantised inputs with the bf16 north-star bound at
+  2048 keys (the quantisation error averages over the keys a row attends to; parity with
+  the reference's SageAttention kernel itself is unpinned: that dependency is absent);
+- LSE: within 2e-4 of the oracle's (fp32 row sums), and of the unsmoothed scores (the
+  q . mean_k correction) within 2e-2 of exact attention.
+"""
+import numpy as np
+import pytest
+import torch
+
+import mod_dit_amd as md  # noqa: F401  (loads the library)
+import oracle as O
+from mod_dit_amd import ops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _randn(shape, seed, dtype, scale=1.0, shift=0.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale + shift).to(dtype).to(DEV)
+
+
+def _z_np(qz, b=0):
+    return dict(q8=qz.q8[b].cpu().numpy(), q_scale=qz.q_scale[b].cpu().numpy(),
+                k8=qz.k8[b].cpu().numpy(), k_scale=qz.k_scale[b].cpu().numpy(),
+                v8t=qz.v8t[b].cpu().numpy(), v_scale=qz.v_scale[b].cpu().numpy(),
+                k_mean=qz.k_mean[b].cpu().numpy(), q_kmean=qz.q_kmean[b].cpu().numpy())
+
+
+def _check_lse(lse, ref, tag, atol):
+    got = _np(lse)
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(got), fin), tag
+    err = np.abs(got[fin] - ref[fin]) if fin.any() else np.zeros(1)
+    print(f"{tag}: LSE max-abs {err.max():.3e}", flush=True)
+    assert err.max() <= atol, (tag, err.max())
+
+
+def _check(out, ref, tag, max_abs, mean_abs):
+    err = np.abs(_np(out).astype(np.float64) - ref)
+    print(f"{tag}: max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
+    assert err.max() <= max_abs and err.mean() <= mean_abs, (tag, err.max(), err.mean())
+
+
+@pytest.mark.parametrize("H,S,D,dtype,strided,origin", [
+    (2, 1000, 128, torch.bfloat16, False, 0),
+    (3, 512, 64, torch.float16, True, 0),
+    (2, 500, 64, torch.bfloat16, False, -14),
+])
+def test_quantize_matches_oracle(H, S, D, dtype, strided, origin):
+    if strided:  # (B,S,H,D) storage viewed as (B,H,S,D)
+        q, k, v = (_randn((1, S, H, D), 10 + i, dtype, shift=0.5 * i).transpose(1, 2)
+                   for i in range(3))
+    else:
+        q, k, v = (_randn((1, H, S, D), 10 + i, dtype, shift=0.5 * i) for i in range(3))
+    qz = ops.quantize_qkv(q, k, v, grid_origin=origin)
+    qz2 = ops.quantize_qkv(q, k, v, grid_origin=origin)
+    for name in ("q8", "q_scale", "k8", "k_scale", "v8t", "v_scale", "k_mean", "q_kmean"):
+        assert torch.equal(getattr(qz, name), getattr(qz2, name)), name  # deterministic
+    kn = _np(k[0]).astype(np.float64)
+    np.testing.assert_allclose(qz.k_mean[0].cpu().numpy(), kn.mean(axis=1), rtol=1e-5, atol=1e-6)
+    ref = O.quantize_qkv(_np(q[0]), _np(k[0]), _np(v[0]), k_mean=qz.k_mean[0].cpu().numpy(),
+                         origin=origin)
+    got = _z_np(qz)
+    for name in ("q8", "q_scale", "k8", "k_scale", "v8t", "v_scale"):
+        assert got[name].shape == ref[name].shape, name
+        assert np.array_equal(got[name], ref[name]), name
+    # fp32 sum of D products: within D ulps of the sum of magnitudes
+    mag = np.einsum("hsd,hd->hs", np.abs(_np(q[0])), np.abs(got["k_mean"]).astype(np.float64))
+    assert np.all(np.abs(got["q_kmean"] - ref["q_kmean"]) <= D * 2.0 ** -24 * mag + 1e-30)
+
+
+@pytest.mark.parametrize("S,D,dtype", [(2048, 128, torch.bfloat16), (2048, 64, torch.float16),
+                                       (1000, 128, torch.bfloat16)])
+def test_q8_dense_attention(S, D, dtype):
+    H = 2
+    q, k, v = (_randn((1, H, S, D), 20 + i, dtype) for i in range(3))
+    qz = ops.quantize_qkv(q, k, v)
+    out, lse = ops.flash_fwd_q8(qz)
+    assert out.dtype == dtype and out.shape == q.shape
+    ref_q, ref_q_lse = O.attention_q8(_z_np(qz))
+    ref, ref_lse = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), None, dtype=np.float64)
+    err = np.abs(_np(out[0]) - ref)
+    print(f"q8 dense vs exact S={S} D={D}: max-abs {err.max():.3e} mean-abs {err.mean():.3e}",
+          flush=True)
+    _check(out[0], ref_q, f"q8 dense vs quantised oracle S={S} D={D}", 4e-3, 2e-4)
+    _check_lse(lse[0], ref_q_lse, f"q8 dense vs quantised oracle S={S} D={D}", 2e-4)
+    if S >= 2048:
+        _check(out[0], ref, f"q8 dense vs exact S={S} D={D}", 2e-2, 2e-3)
+        _check_lse(lse[0], ref_lse, f"q8 dense vs exact S={S} D={D}", 2e-2)
+    out2, _ = ops.flash_fwd_q8(qz)
+    assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("union", [False, True])
+def test_q8_block_sparse_attention(union):
+    H, S, D, bs = 2, 2048, 128, 64
+    q, k, v = (_randn((1, H, S, D), 30 + i, torch.bfloat16) for i in range(3))
+    rng = np.random.default_rng(3)
+    m = rng.random((H, S // bs, S // bs)) < 0.4
+    m[:, np.arange(S // bs), np.arange(S // bs)] = True
+    m[:, 5, :] = False  # a block row with no keys
+    tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=union)
+    qz = ops.quantize_qkv(q, k, v)
+    out, lse = ops.block_sparse_fwd_q8(qz, tiles, return_lse=True)
+    c = tiles.counts.cpu().numpy()
+    e = tiles.entries.cpu().numpy()
+    lists = [[[int(x) for x in e[h, t, :c[h, t]]] for t in range(c.shape[1])] for h in range(H)]
+    tm = O.token_mask_from_tiles(lists, H, S, S)
+    ref_q, ref_lse = O.attention_q8(_z_np(qz), tm)
+    _check(out[0], ref_q, f"q8 sparse vs quantised oracle union={union}", 4e-3, 2e-4)
+    _check_lse(lse[0], ref_lse, f"q8 sparse vs quantised oracle union={union}", 2e-4)
+    if not union:  # with union rows, block row 5 shares its 128-row tile with row 4's keys
+        assert torch.all(out[0, :, 5 * bs:6 * bs] == 0)
+        assert torch.all(torch.isneginf(lse[0, :, 5 * bs:6 * bs]))
+
+
+def test_q8_shifted_grid_cogvideox_layout():
+    # 50 text + 450 video tokens: tiles on the grid that starts 14 tokens before token 0
+    H, D, bs, text, video = 2, 64, 64, 50, 450
+    S = text + video
+    tb, vb, origin = O.cogvideox_grid(text, video, bs)
+    q, k, v = (_randn((1, H, S, D), 40 + i, torch.bfloat16) for i in range(3))
+    rng = np.random.default_rng(4)
+    m = rng.random((H, tb + vb, tb + vb)) < 0.5
+    m[:, :, 0] = True
+    tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=False, grid_origin=origin)
+    with pytest.raises(ValueError, match="grid"):
+        ops.block_sparse_fwd_q8(ops.quantize_qkv(q, k, v), tiles)  # quantised on another grid
+    qz = ops.quantize_qkv(q, k, v, grid_origin=origin)
+    out, lse = ops.block_sparse_fwd_q8(qz, tiles, return_lse=True)
+    _, lists = O.tiles_from_mask(m, bs, union_rows=False)
+    tm = O.token_mask_from_tiles(lists, H, S, S, origin=origin)
+    ref_q, ref_lse = O.attention_q8(_z_np(qz), tm, origin=origin)
+    _check(out[0], ref_q, "q8 shifted grid vs quantised oracle", 4e-3, 3e-4)
+    _check_lse(lse[0], ref_lse, "q8 shifted grid vs quantised oracle", 2e-4)

@@ -341,3 +341,119 @@ def test_step_schedule_W12_T10():
     assert phases[10] == "map_fit" and phases[11] == "map_fit_predict"
     assert [s for s, p in enumerate(phases) if p == "refresh"] == [21, 31, 41]
     assert phases.count("sparse") == 50 - 12 - 3
+
+
+# ------------------------------------------------------------------ int8 / fp8 path --
+def test_e4m3_known_answers_and_ties():
+    # OCP FP8 E4M3: 0x38 = 1.0, 0x7e = 448 (max), 0x08 = 2^-6 (min normal), 0x01 = 2^-9
+    dec = O.e4m3_decode(np.array([0x38, 0x7E, 0x08, 0x01, 0xB8, 0x00, 0x7F], np.uint8))
+    assert dec[:6].tolist() == [1.0, 448.0, 2.0 ** -6, 2.0 ** -9, -1.0, 0.0] and np.isnan(dec[6])
+    # every finite code round-trips; midpoints round to the even code
+    codes = np.arange(256, dtype=np.uint8)
+    vals = O.e4m3_decode(codes)
+    ok = np.isfinite(vals) & (codes != 0x80)
+    assert np.array_equal(O.e4m3_encode(vals[ok]), codes[ok])
+    assert O.e4m3_encode(np.array([1.0625]))[0] == 0x38      # tie between 0x38 and 0x39
+    assert O.e4m3_encode(np.array([1.1875]))[0] == 0x3A      # tie between 0x39 and 0x3a
+    assert O.e4m3_encode(np.array([1.0625 + 1e-9]))[0] == 0x39
+
+
+@pytest.mark.parametrize("origin", [0, -14])
+def test_quantize_qkv_bounds(origin):
+    rng = np.random.default_rng(8)
+    H, S, D = 2, 200, 64
+    q = O.bf16_round(rng.standard_normal((H, S, D)) * 2)
+    k = O.bf16_round(rng.standard_normal((H, S, D)) + 3.0)  # channel offset removed by the mean
+    v = O.bf16_round(rng.standard_normal((H, S, D)))
+    z = O.quantize_qkv(q, k, v, origin=origin)
+    pos = np.arange(S) - origin  # grid position of each token
+    qs = z["q_scale"][:, pos // 32][:, :, None]
+    assert np.abs(q - z["q8"] * qs).max() <= 0.5001 * qs.max()
+    assert np.abs(z["q8"]).max() == 127
+    ks = z["k_scale"][:, pos // 64][:, :, None]
+    kd = z["k8"] * ks + z["k_mean"][:, None, :]
+    assert np.abs(k - kd).max() <= 0.5001 * ks.max() + 1e-5
+    vd = O.e4m3_decode(z["v8t"][:, :, pos]).transpose(0, 2, 1) * z["v_scale"][:, None, :]
+    assert np.all(np.abs(v - vd) <= 2.0 ** -4 * np.abs(v) + 2.0 ** -9 * z["v_scale"].max())
+    outside = np.ones(z["v8t"].shape[2], bool)
+    outside[pos] = False
+    assert np.all(z["v8t"][:, :, outside] == 0)  # grid positions outside the sequence
+    np.testing.assert_allclose(z["k_mean"], k.mean(axis=1), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(z["q_kmean"], np.einsum("hsd,hd->hs", q, z["k_mean"].astype(np.float64)),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_quantize_qkv_shifted_grid_is_zero_padding():
+    # on the grid starting at -14, Q and V are quantised as the sequence with 14 zero tokens
+    # in front on the unshifted grid; K as its mean-free part padded with zeros
+    rng = np.random.default_rng(18)
+    H, S, D, pad = 2, 150, 64, 14
+    q, k, v = (O.bf16_round(rng.standard_normal((H, S, D)) * 1.5) for _ in range(3))
+    km = k.mean(axis=1).astype(np.float32)
+    z = O.quantize_qkv(q, k, v, origin=-pad)
+    zp = lambda x: np.concatenate([np.zeros((H, pad, D), np.float32), x], axis=1)
+    ref = O.quantize_qkv(zp(q), zp(k - km[:, None, :]), zp(v), k_mean=np.zeros_like(km))
+    assert np.array_equal(z["q8"], ref["q8"][:, pad:])
+    assert np.array_equal(z["q_scale"], ref["q_scale"])
+    assert np.array_equal(z["v8t"][:, :, :S + pad], ref["v8t"][:, :, :S + pad])
+    assert np.array_equal(z["k_scale"], ref["k_scale"])
+    assert np.abs(z["k8"].astype(int) - ref["k8"][:, pad:]).max() <= 1  # k - mean rounded once
+
+
+@pytest.mark.parametrize("origin", [0, -14])
+def test_attention_q8_is_close_to_exact_attention(origin):
+    # the quantisation error averages over the keys a row attends to: with 2048 keys it is
+    # inside the bf16 bound (at 256 keys fp8 P alone reaches max-abs 0.011, all three 0.034)
+    rng = np.random.default_rng(9)
+    H, S, D = 2, 2048, 64
+    q, k, v = (O.bf16_round(rng.standard_normal((H, S, D))) for _ in range(3))
+    k = k + O.bf16_round(rng.standard_normal((H, 1, D)) * 0.5)  # a channel offset
+    z = O.quantize_qkv(q, k, v, origin=origin)
+    ref, ref_lse = O.masked_attention(q, k, v, None, dtype=np.float64)
+    got, lse = O.attention_q8(z, origin=origin)
+    err = np.abs(got - ref)
+    assert err.max() < 2e-2 and err.mean() < 2e-3, (err.max(), err.mean())
+    # the LSE of the unsmoothed scores: without the q . mean_k term it is off by ~0.2
+    assert np.abs(lse - ref_lse).max() < 1e-2
+    assert np.abs(lse - D ** -0.5 * z["q_kmean"] - ref_lse).max() > 0.1
+    # uniform scores (q = 0): the output is the mean of the dequantised V
+    z0 = O.quantize_qkv(np.zeros_like(q), k, v, origin=origin)
+    pos = np.arange(S) - origin
+    vd = O.e4m3_decode(z0["v8t"][:, :, pos]).transpose(0, 2, 1) * z0["v_scale"][:, None, :]
+    o0, l0 = O.attention_q8(z0, origin=origin)
+    np.testing.assert_allclose(o0, np.broadcast_to(vd.mean(1, keepdims=True), vd.shape),
+                               rtol=0, atol=1e-12)
+    np.testing.assert_allclose(l0, np.log(S), rtol=0, atol=1e-12)
+
+
+def test_attention_q8_lazy_max_and_masks():
+    # Against exact masked attention on the dequantised values, the only error left is the
+    # e4m3 rounding of P (relative 2^-4 for normal values; absolute 2^-10 below 2^-6, where
+    # the row sum is at least 2^(7-1.5)): |O - O_exact| <= 2^-4 sum_k w_k |v_k| +
+    # 2^-15.5 sum_k |v_k|, whatever the slack; the LSE is exact (row sums of unrounded P).
+    # A row with no keys has O = 0 and LSE = -inf.
+    rng = np.random.default_rng(19)
+    H, S, D = 1, 256, 64
+    q, k, v = (O.bf16_round(rng.standard_normal((H, S, D)) * 2) for _ in range(3))
+    z = O.quantize_qkv(q, k, v)
+    tm = np.ones((H, S, S), bool)
+    tm[:, 3, :] = False
+    tm[:, :, 200:] = False
+    r = np.arange(S)
+    qd = z["q8"] * z["q_scale"][:, r // 32][:, :, None].astype(np.float64)
+    kd = z["k8"] * z["k_scale"][:, r // 64][:, :, None].astype(np.float64)
+    vd = O.e4m3_decode(z["v8t"][:, :, :S]).transpose(0, 2, 1) * z["v_scale"][:, None, :]
+    ref_o, ref_l = O.masked_attention(qd, kd, vd, tm, dtype=np.float64)
+    w, _ = O.masked_attention(qd, kd, np.eye(S)[None].repeat(H, 0), tm, dtype=np.float64)
+    bound = 2.0 ** -4 * (w @ np.abs(vd)) + 2.0 ** -15.5 * (tm.astype(float) @ np.abs(vd))
+    keep = np.ones(S, bool)
+    keep[3] = False
+    # (slack <= log2(448) - 7 keeps P = 2^(s - m + 7) inside e4m3's range)
+    for slack in (0.0, 0.75, 1.5):
+        o, l = O.attention_q8(z, tm, slack=slack)
+        assert np.all(o[:, 3] == 0) and np.isneginf(l[:, 3]).all()
+        assert np.all(np.abs(o - ref_o)[:, keep] <= bound[:, keep] + 1e-12), slack
+        np.testing.assert_allclose(l[:, keep] - D ** -0.5 * z["q_kmean"][:, keep], ref_l[:, keep],
+                                   rtol=0, atol=1e-9)
+    # the bound is not loose by orders of magnitude: the rounding error does show
+    assert np.abs(o - ref_o)[:, keep].max() > 0.05 * bound[:, keep].max()
