@@ -142,8 +142,10 @@ int moddit_quantize_workspace_floats(int batch, int heads, int head_dim);
  * q_scale * k_scale, fp32 online softmax, P rounded to e4m3 for the fp8 P.V product,
  * O = (P.V8) * v_scale[d] / rowsum written as dtype (bf16/fp16) with the given strides,
  * natural-log LSE (may be NULL; needs q_kmean when not). moddit_block_sparse_fwd_q8 takes
- * the tile lists and grid origin of moddit_block_sparse_fwd; the quantisation must have
- * used the same grid_origin (the dense kernel: 0).
+ * the tile lists and grid origin of moddit_block_sparse_fwd (the quantisation must have
+ * used the same grid_origin; the dense kernel: 0), and q_len <= seq_len: queries
+ * 0..q_len-1 attend to all seq_len keys (the reference's video-query prefix against the
+ * full key set, attn_mask.py:312-317); o and lse hold q_len rows, n_qtiles covers them.
  * Replaces block_sparse_sage2_attn_cuda (MoD/mod/attn_mask.py:306,312-317) and sageattn
  * (attn_mask.py:271-276) with their own quantised arithmetic (parity unpinned against
  * them; pinned against exact attention on the dequantised inputs).
@@ -156,7 +158,7 @@ int moddit_flash_fwd_q8(const int8_t* q8, const float* q_scale, const int8_t* k8
 int moddit_block_sparse_fwd_q8(const int8_t* q8, const float* q_scale, const int8_t* k8,
                                const float* k_scale, const uint8_t* v8t, const float* v_scale,
                                const float* q_kmean, void* o, float* lse, int batch, int heads,
-                               int seq_len, int head_dim, const int64_t o_strides[3],
+                               int seq_len, int q_len, int head_dim, const int64_t o_strides[3],
                                float softmax_scale, int dtype, const int32_t* counts,
                                const int32_t* entries, int n_qtiles, int cap, int grid_origin,
                                moddit_stream_t stream);

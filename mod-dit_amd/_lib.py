@@ -43,7 +43,7 @@ _SIGNATURES = {
     "moddit_flash_fwd_q8": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                                  _c_i64p, _f, _i, _vp]),
     "moddit_block_sparse_fwd_q8": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i,
-                                        _i, _c_i64p, _f, _i, _vp, _vp, _i, _i, _i, _vp]),
+                                        _i, _i, _c_i64p, _f, _i, _vp, _vp, _i, _i, _i, _vp]),
     "moddit_sparsity_map": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _c_i64p, _c_i64p,
                                  _f, _f, _i, _i, _i, _i, _i, _vp]),
     "moddit_mts": (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),

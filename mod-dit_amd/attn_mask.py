@@ -11,15 +11,19 @@ Differences that are deliberate:
   * no host synchronisation on the path: head modes stay on the device (HeadModes
     behaves like the reference's list of strings when read), the block-diagonal test,
     line selection, mask construction and the refresh merge are device kernels, and the
-    engine never calls mask.all();
+    engine never calls mask.all(): an all-True mask runs block-sparse like any other (with
+    a Hunyuan padding mask its video queries then also see the padded keys of the last
+    64-key tile, as in the reference's sparse branch, where its dense branch would stop at
+    the valid keys);
   * selected lines come back in ascending index order (the reference's
     topk(sorted=False) order is unspecified); ties at the k-th value go to the lower
     index;
   * the mask kernel also emits the attention tile lists, so sparse steps do not
     convert the mask again;
-  * sparse types other than 'mod-dit' ('radial', 'spargeattn') and the Hunyuan text
-    tail of the sparse engine call third-party kernels in the reference and raise
-    NotImplementedError here.
+  * sparse types other than 'mod-dit' ('radial', 'spargeattn') call third-party kernels
+    in the reference and raise NotImplementedError here;
+  * the engine's arithmetic is bf16 by default; the state key 'precision' = 'int8'
+    selects the reference engine's quantised (SageAttention2-style) numerics.
 """
 from __future__ import annotations
 
@@ -250,14 +254,19 @@ def _kv_valid(pre_defined_mask: torch.Tensor) -> int:
 
 
 def _engine(query, key, value, mask, tiles, pre_defined_mask, video_token_num, block_size,
-            union_rows, grid_origin=0):
+            union_rows, grid_origin=0, precision="bf16"):
     if mask.dim() == 2:
         mask = mask.unsqueeze(0).expand(query.shape[1], -1, -1)
+    q8 = precision == "int8"
     if pre_defined_mask is None:
         if tiles is None:
             tiles = ops.mask_to_tiles(mask, block_size, union_rows=union_rows,
                                       grid_origin=grid_origin)
-        out, _ = ops.block_sparse_fwd(query, key, value, tiles)
+        if q8:
+            qz = ops.quantize_qkv(query, key, value, grid_origin=grid_origin)
+            out, _ = ops.block_sparse_fwd_q8(qz, tiles)
+        else:
+            out, _ = ops.block_sparse_fwd(query, key, value, tiles)
         return out
     # Hunyuan layout (MoD/mod/attn_mask.py:310-331): video queries run block-sparse over the
     # key tiles below ceil(valid/64) (so up to 63 padded text keys of the last tile take
@@ -272,9 +281,13 @@ def _engine(query, key, value, mask, tiles, pre_defined_mask, video_token_num, b
     if video > 0:
         vt = ops.mask_to_tiles(mask[:, :video // block_size, :], block_size, union_rows=union_rows,
                                kv_tiles=kv_tiles)
-        kv_len = min(S, kv_tiles * 64)
-        ops.block_sparse_fwd(query[:, :, :video], key[:, :, :kv_len], value[:, :, :kv_len], vt,
-                             out=out[:, :, :video])
+        if q8:  # the whole sequence is quantised, as the reference passes the full key/value
+            qz = ops.quantize_qkv(query, key, value)
+            ops.block_sparse_fwd_q8(qz, vt, out=out[:, :, :video], q_len=video)
+        else:
+            kv_len = min(S, kv_tiles * 64)
+            ops.block_sparse_fwd(query[:, :, :video], key[:, :, :kv_len], value[:, :, :kv_len], vt,
+                                 out=out[:, :, :video])
     if video < S:
         ops.flash_fwd(query[:, :, video:], key[:, :, :kv], value[:, :, :kv], return_lse=False,
                       out=out[:, :, video:])
@@ -282,14 +295,19 @@ def _engine(query, key, value, mask, tiles, pre_defined_mask, video_token_num, b
 
 
 def AttentionSparseEngine(query, key, value, mask, pre_defined_mask=None, video_token_num=0,
-                          block_size=128, union_rows: bool = True):
+                          block_size=128, union_rows: bool = True, precision: str = "bf16"):
     """Block-sparse attention under a bool block mask; MoD/mod/attn_mask.py:266-331.
 
     union_rows=True executes each pair of 64-row mask rows as one 128-row query tile over
     the union of their key blocks, which is what the reference engine runs (:299-303).
+    precision='int8' runs the int8 Q.K^T / fp8 P.V kernels on the video queries (the
+    reference's block_sparse_sage2_attn_cuda numerics, :306,312-317); text queries of a
+    padded (Hunyuan) layout stay bf16, as the reference's flashinfer call is (:319-330).
     """
+    if precision not in ("bf16", "int8"):
+        raise ValueError(f"precision must be 'bf16' or 'int8', got {precision!r}")
     return _engine(query, key, value, mask, None, pre_defined_mask, video_token_num,
-                   block_size, union_rows)
+                   block_size, union_rows, precision=precision)
 
 
 def _dense_engine(query, key, value, pre_defined_mask):
@@ -400,5 +418,6 @@ def SparseAttentionWithMap(
         output = _engine(query, key, value, mask, tiles, pre_defined_mask,
                          warmup_state.get("video_token_num", 0), warmup_state["block_size"],
                          warmup_state.get("tile_rows", "union") == "union",
-                         grid_origin=_grid(warmup_state, seq_len)[3])
+                         grid_origin=_grid(warmup_state, seq_len)[3],
+                         precision=warmup_state.get("precision", "bf16"))
     return output, {"mask": warmup_state["mask"]}

@@ -67,7 +67,8 @@ struct Q8Params {
   float* lse;
   int64_t o_sb, o_sh, o_ss;
   int heads;
-  int seq_len;
+  int seq_len;  // keys (and the quantised tensors' rows)
+  int q_len;    // queries: rows 0..q_len-1 (a prefix of the quantised rows)
   int s_pad;
   int origin;
   int n_qtiles;
@@ -425,7 +426,7 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
 
   // ---- epilogue: O = O^T * v_scale[d] / l ----
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  if (q_row >= 0 && q_row < p.seq_len) {
+  if (q_row >= 0 && q_row < p.q_len) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const float* vsc = p.v_scale + static_cast<int64_t>(bh) * D;
     const int b = bh / p.heads;
@@ -446,9 +447,10 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
     }
     if (p.lse != nullptr && half == 0) {
       // LSE of the unsmoothed scores: + scale * q . mean_k
-      const int64_t li = static_cast<int64_t>(bh) * p.seq_len + q_row;
+      const int64_t li = static_cast<int64_t>(bh) * p.q_len + q_row;
+      const float corr = p.q_kmean[static_cast<int64_t>(bh) * p.seq_len + q_row];
       p.lse[li] = l_tot > 0.f ? __builtin_fmaf(m_run - kPShift + log2f(l_tot), 0.69314718055994531f,
-                                               p.scale * p.q_kmean[li])
+                                               p.scale * corr)
                               : -INFINITY;
     }
   }
@@ -489,7 +491,8 @@ int launch_q8(const Q8Params& p, int batch, hipStream_t stream) {
 int q8_entry(const int8_t* q8, const float* q_scale, const int8_t* k8, const float* k_scale,
              const uint8_t* v8t, const float* v_scale, const float* q_kmean, void* o, float* lse,
              int batch,
-             int heads, int seq_len, int head_dim, const int64_t* os, float scale, int dtype,
+             int heads, int seq_len, int q_len, int head_dim, const int64_t* os, float scale,
+             int dtype,
              const int32_t* counts, const int32_t* entries, int n_qtiles, int cap, int origin,
              moddit_stream_t stream) {
   clear_error();
@@ -499,6 +502,8 @@ int q8_entry(const int8_t* q8, const float* q_scale, const int8_t* k8, const flo
                    "attention_q8: the LSE needs q_kmean (the quantiser's q . mean_k)");
   MODDIT_CHECK_ARG(scale > 0.f && std::isfinite(scale), "attention_q8: softmax_scale must be positive");
   MODDIT_CHECK_ARG(batch >= 0 && heads >= 0 && seq_len >= 0, "attention_q8: negative size");
+  MODDIT_CHECK_ARG(q_len >= 0 && q_len <= seq_len,
+                   "attention_q8: q_len=%d must lie in [0, seq_len=%d]", q_len, seq_len);
   if (head_dim != 64 && head_dim != 128) {
     set_error("attention_q8: head_dim must be 64 or 128, got %d", head_dim);
     return MODDIT_EUNSUPPORTED;
@@ -515,14 +520,14 @@ int q8_entry(const int8_t* q8, const float* q_scale, const int8_t* k8, const flo
     MODDIT_CHECK_ARG(os[j] >= 0 && os[j] % 8 == 0,
                      "attention_q8: output strides must be non-negative multiples of 8");
   const bool sparse = counts != nullptr;
-  const int nq = (seq_len - origin + kBM - 1) / kBM;
+  const int nq = (q_len - origin + kBM - 1) / kBM;
   if (sparse) {
     MODDIT_CHECK_ARG(entries != nullptr, "attention_q8: tile entries missing");
     MODDIT_CHECK_ARG(n_qtiles == nq, "attention_q8: n_qtiles=%d but the sequence needs %d",
                      n_qtiles, nq);
     MODDIT_CHECK_ARG(cap > 0, "attention_q8: cap must be positive");
   }
-  if (seq_len == 0 || batch == 0 || heads == 0) return MODDIT_OK;
+  if (q_len == 0 || batch == 0 || heads == 0) return MODDIT_OK;
   Q8Params p;
   p.q8 = q8;
   p.q_scale = q_scale;
@@ -536,6 +541,7 @@ int q8_entry(const int8_t* q8, const float* q_scale, const int8_t* k8, const flo
   p.o_sb = os[0]; p.o_sh = os[1]; p.o_ss = os[2];
   p.heads = heads;
   p.seq_len = seq_len;
+  p.q_len = q_len;
   p.s_pad = (seq_len - origin + kBN - 1) / kBN * kBN;
   p.origin = origin;
   p.n_qtiles = nq;
@@ -574,16 +580,15 @@ extern "C" int moddit_flash_fwd_q8(const int8_t* q8, const float* q_scale, const
                                    const int64_t o_strides[3], float softmax_scale, int dtype,
                                    moddit_stream_t stream) {
   return moddit::q8_entry(q8, q_scale, k8, k_scale, v8t, v_scale, q_kmean, o, lse, batch, heads, seq_len,
-                          head_dim, o_strides, softmax_scale, dtype, nullptr, nullptr, 0, 0, 0,
-                          stream);
+                          seq_len, head_dim, o_strides, softmax_scale, dtype, nullptr, nullptr, 0,
+                          0, 0, stream);
 }
 
 extern "C" int moddit_block_sparse_fwd_q8(const int8_t* q8, const float* q_scale,
                                           const int8_t* k8, const float* k_scale,
                                           const uint8_t* v8t, const float* v_scale,
                                           const float* q_kmean, void* o, float* lse, int batch,
-                                          int heads, int seq_len,
-                                          int head_dim, const int64_t o_strides[3],
+                                          int heads, int seq_len, int q_len, int head_dim, const int64_t o_strides[3],
                                           float softmax_scale, int dtype, const int32_t* counts,
                                           const int32_t* entries, int n_qtiles, int cap,
                                           int grid_origin, moddit_stream_t stream) {
@@ -592,6 +597,6 @@ extern "C" int moddit_block_sparse_fwd_q8(const int8_t* q8, const float* q_scale
     return MODDIT_EINVAL;
   }
   return moddit::q8_entry(q8, q_scale, k8, k_scale, v8t, v_scale, q_kmean, o, lse, batch, heads, seq_len,
-                          head_dim, o_strides, softmax_scale, dtype, counts, entries, n_qtiles,
-                          cap, grid_origin, stream);
+                          q_len, head_dim, o_strides, softmax_scale, dtype, counts, entries,
+                          n_qtiles, cap, grid_origin, stream);
 }

@@ -215,11 +215,17 @@ def quantize_qkv(q, k, v, grid_origin: int = 0) -> QuantizedQKV:
     return out
 
 
-def _attention_q8(qz: QuantizedQKV, scale, return_lse, tiles: TileList | None, out=None):
+def _attention_q8(qz: QuantizedQKV, scale, return_lse, tiles: TileList | None, out=None,
+                  q_len=None):
     B, H, S, D = qz.shape
+    q_len = S if q_len is None else int(q_len)
+    if not 0 <= q_len <= S:
+        raise ValueError(f"q_len={q_len} must lie in [0, {S}]")
     if out is None:
-        out = torch.empty((B, H, S, D), device=qz.q8.device, dtype=qz.dtype)
-    lse = torch.empty((B, H, S), device=out.device, dtype=torch.float32) if return_lse else None
+        out = torch.empty((B, H, q_len, D), device=qz.q8.device, dtype=qz.dtype)
+    if tuple(out.shape) != (B, H, q_len, D) or out.dtype != qz.dtype:
+        raise ValueError(f"out must be {qz.dtype} of shape {(B, H, q_len, D)}")
+    lse = torch.empty((B, H, q_len), device=out.device, dtype=torch.float32) if return_lse else None
     if scale is None:
         scale = D ** -0.5
     dt = _attn_dtype(out)
@@ -228,17 +234,18 @@ def _attention_q8(qz: QuantizedQKV, scale, return_lse, tiles: TileList | None, o
     if qz.origin != origin:
         raise ValueError(f"q/k/v were quantised on the grid starting at {qz.origin}, the "
                          f"attention runs on the grid starting at {origin}")
-    args = (qz.q8.data_ptr(), qz.q_scale.data_ptr(), qz.k8.data_ptr(), qz.k_scale.data_ptr(),
+    head = (qz.q8.data_ptr(), qz.q_scale.data_ptr(), qz.k8.data_ptr(), qz.k_scale.data_ptr(),
             qz.v8t.data_ptr(), qz.v_scale.data_ptr(), qz.q_kmean.data_ptr(), out.data_ptr(),
-            _ptr(lse), B, H, S, D, strides3(*out.stride()[:3]), float(scale), dt)
+            _ptr(lse), B, H, S)
+    tail = (D, strides3(*out.stride()[:3]), float(scale), dt)
     if tiles is None:
-        check(lib.moddit_flash_fwd_q8(*args, _stream(out)), "moddit_flash_fwd_q8")
+        check(lib.moddit_flash_fwd_q8(*head, *tail, _stream(out)), "moddit_flash_fwd_q8")
     else:
         if tiles.counts.shape[0] != H:
             raise ValueError(f"tile lists cover {tiles.counts.shape[0]} heads, attention has {H}")
-        check(lib.moddit_block_sparse_fwd_q8(*args, tiles.counts.data_ptr(),
+        check(lib.moddit_block_sparse_fwd_q8(*head, q_len, *tail, tiles.counts.data_ptr(),
                                              tiles.entries.data_ptr(), tiles.n_qtiles, tiles.cap,
-                                             int(tiles.origin), _stream(out)),
+                                             origin, _stream(out)),
               "moddit_block_sparse_fwd_q8")
     return out, lse
 
@@ -249,9 +256,10 @@ def flash_fwd_q8(qz: QuantizedQKV, softmax_scale=None, return_lse=True, out=None
 
 
 def block_sparse_fwd_q8(qz: QuantizedQKV, tiles: TileList, softmax_scale=None, return_lse=False,
-                        out=None):
-    """Block-sparse int8/fp8 attention over the active key tiles of `tiles`."""
-    return _attention_q8(qz, softmax_scale, return_lse, tiles, out)
+                        out=None, q_len=None):
+    """Block-sparse int8/fp8 attention over the active key tiles of `tiles`; with `q_len`
+    only queries 0..q_len-1 attend (to all keys), and O / LSE hold q_len rows."""
+    return _attention_q8(qz, softmax_scale, return_lse, tiles, out, q_len)
 
 
 # --------------------------------------------------------------------------------------

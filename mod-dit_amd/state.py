@@ -1,10 +1,14 @@
 """Per-layer state of the MOD-DiT step machine (MoD/mod/state.py:3-71).
 
-Same keys and validation as the reference, plus two keys of this build:
+Same keys and validation as the reference, plus keys of this build:
   'tile_rows'  'union' (default): the attention engine runs each mask row pair as one
                128-row query tile over the union of both rows' key blocks, as the
                reference's engine does (MoD/mod/attn_mask.py:299-303);
                'exact': 64x64 blocks are honoured exactly.
+  'precision'  arithmetic of the sparse steps' attention: 'bf16' (default; bf16 MFMA,
+               fp32 softmax) or 'int8' (int8 Q.K^T with smoothed K, fp8 e4m3 P.V: the
+               SageAttention2-style numerics of the reference's engine,
+               MoD/mod/attn_mask.py:306,312-317). Map steps always run bf16.
   '_tiles'     the attention tile lists built together with 'mask'.
 """
 from __future__ import annotations
@@ -41,6 +45,7 @@ def create_adaptive_mask_state(
     use_cuda: bool = True,
     sparse_type: str = "mod-dit",
     tile_rows: str = "union",
+    precision: str = "bf16",
 ) -> Dict:
     """Build a layer state (MoD/mod/state.py:24-68)."""
     state = init_warmup_state()
@@ -65,6 +70,9 @@ def create_adaptive_mask_state(
     if tile_rows not in ("union", "exact"):
         raise ValueError(f"tile_rows must be 'union' or 'exact', got {tile_rows!r}")
     state["tile_rows"] = tile_rows
+    if precision not in ("bf16", "int8"):
+        raise ValueError(f"precision must be 'bf16' or 'int8', got {precision!r}")
+    state["precision"] = precision
     return state
 
 

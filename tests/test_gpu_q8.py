@@ -147,3 +147,106 @@ def test_q8_shifted_grid_cogvideox_layout():
     ref_q, ref_lse = O.attention_q8(_z_np(qz), tm, origin=origin)
     _check(out[0], ref_q, "q8 shifted grid vs quantised oracle", 4e-3, 3e-4)
     _check_lse(lse[0], ref_lse, "q8 shifted grid vs quantised oracle", 2e-4)
+
+
+def test_q8_query_prefix():
+    # queries 0..q_len-1 attend to all keys (the reference's video-query prefix against the
+    # full key set); O and LSE hold q_len rows
+    H, S, D, bs, q_len = 2, 1000, 64, 64, 640
+    q, k, v = (_randn((1, H, S, D), 50 + i, torch.bfloat16) for i in range(3))
+    rng = np.random.default_rng(5)
+    m = rng.random((H, q_len // bs, (S + bs - 1) // bs)) < 0.4
+    m[:, :, 0] = True
+    tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=True)
+    qz = ops.quantize_qkv(q, k, v)
+    out, lse = ops.block_sparse_fwd_q8(qz, tiles, return_lse=True, q_len=q_len)
+    assert out.shape == (1, H, q_len, D) and lse.shape == (1, H, q_len)
+    _, lists = O.tiles_from_mask(m, bs, union_rows=True)
+    tm = np.zeros((H, S, S), bool)
+    tm[:, :q_len] = O.token_mask_from_tiles(lists, H, q_len, S)
+    ref_q, ref_lse = O.attention_q8(_z_np(qz), tm)
+    _check(out[0], ref_q[:, :q_len], "q8 query prefix vs quantised oracle", 4e-3, 2e-4)
+    _check_lse(lse[0], ref_lse[:, :q_len], "q8 query prefix vs quantised oracle", 2e-4)
+    with pytest.raises(ValueError, match="q_len"):
+        ops.block_sparse_fwd_q8(qz, tiles, q_len=S + 1)
+
+
+def _sparse_mask(H, n, seed, p=0.35):
+    rng = np.random.default_rng(seed)
+    m = rng.random((H, n, n)) < p
+    m[:, np.arange(n), np.arange(n)] = True
+    return m
+
+
+@pytest.mark.parametrize("layout", ["wan", "hunyuan"])
+def test_engine_int8_precision(layout):
+    """AttentionSparseEngine(precision='int8'): video queries on the quantised kernels (the
+    reference engine's block_sparse_sage2_attn_cuda numerics), against the oracle on the
+    same quantised tensors; Hunyuan text queries stay bf16 (exact attention, bf16 bound)."""
+    import mod_dit_amd as md
+    H, D, bs = 2, 64, 64
+    if layout == "wan":
+        video, text, valid = 2048, 0, 2048
+    else:
+        video, text, valid = 1536, 256, 1536 + 150
+    S = video + text
+    q, k, v = (_randn((1, H, S, D), 60 + i, torch.bfloat16) for i in range(3))
+    n = S // bs
+    m = _sparse_mask(H, n, 6)
+    pdm = None
+    if layout == "hunyuan":
+        m[:, video // bs:, :] = True
+        m[:, :, video // bs:] = True
+        pdm = torch.zeros(S, S, dtype=torch.bool, device=DEV)
+        pdm[:, :valid] = True
+    out = md.AttentionSparseEngine(q, k, v, torch.from_numpy(m).to(DEV), pre_defined_mask=pdm,
+                                   video_token_num=video, block_size=bs, precision="int8")
+    qz = ops.quantize_qkv(q, k, v)  # deterministic: the tensors the engine quantised
+    kv_tiles = (valid + 63) // 64 if layout == "hunyuan" else None
+    _, lists = O.tiles_from_mask(m[:, :video // bs], bs, True, kv_tiles=kv_tiles)
+    tm = np.zeros((H, S, S), bool)
+    tm[:, :video] = O.token_mask_from_tiles(lists, H, video, S)
+    ref_q, _ = O.attention_q8(_z_np(qz), tm)
+    _check(out[0, :, :video], ref_q[:, :video], f"engine int8 {layout} video rows", 4e-3, 2e-4)
+    if text:
+        ref, _ = O.masked_attention(_np(q[0]), _np(k[0, :, :valid]), _np(v[0, :, :valid]), None,
+                                    dtype=np.float64)
+        _check(out[0, :, video:], ref[:, video:], f"engine int8 {layout} text rows", 2e-2, 2e-3)
+    with pytest.raises(ValueError, match="precision"):
+        md.AttentionSparseEngine(q, k, v, torch.from_numpy(m).to(DEV), precision="fp4")
+
+
+def test_schedule_int8_precision_cogvideox_shifted_grid():
+    """create_adaptive_mask_state(precision='int8'): sparse steps of an unaligned CogVideoX
+    layout (grid starting 14 tokens before the text) run the quantised kernels on the
+    shifted grid; map steps stay bf16."""
+    import mod_dit_amd as md
+    H, D, bs = 2, 64, 64
+    text, F, tpf = 50, 3, 150
+    video = F * tpf
+    S = text + video
+    W, T = 4, 3
+    tb, vb, origin = O.cogvideox_grid(text, video, bs)
+    st = md.create_adaptive_mask_state("cogvideox", H, video, text, tpf, F, warmup_steps=W,
+                                       top_k=6, predict_T=T, threshold=1e-3, block_size=bs,
+                                       tile_rows="union", precision="int8")
+    checked = 0
+    for step in range(W + 2):
+        g = torch.Generator().manual_seed(70 + step)
+        q, k, v = ((torch.randn(1, H, S, D, generator=g)).to(torch.bfloat16).to(DEV)
+                   for _ in range(3))
+        phase = O.step_phase(step, W, T)
+        out, _ = md.SparseAttentionWithMap(q, k, v, st, None, current_step=step,
+                                           use_dense=step < W - 2)
+        if phase != "sparse":
+            continue
+        mask = st["mask"].cpu().numpy()
+        _, lists = O.tiles_from_mask(mask, bs, True)
+        tm = O.token_mask_from_tiles(lists, H, S, S, origin=origin)
+        qz = ops.quantize_qkv(q, k, v, grid_origin=origin)
+        ref_q, _ = O.attention_q8(_z_np(qz), tm, origin=origin)
+        _check(out[0], ref_q, f"cogvideox int8 sparse step {step}", 4e-3, 3e-4)
+        checked += 1
+    assert checked == 2
+    with pytest.raises(ValueError, match="precision"):
+        md.create_adaptive_mask_state("wan", 2, 1024, 0, 512, 2, precision="fp8")
