@@ -26,7 +26,7 @@ namespace moddit {
 namespace {
 
 constexpr int kQThreads = 256;
-constexpr int kStatChunks = 16;  // partial column statistics per (b, h)
+constexpr int kStatChunks = 64;  // row ranges per (b, h) with partial column statistics
 
 struct StatParams {
   const uint16_t* k;
@@ -36,15 +36,20 @@ struct StatParams {
   int heads;
   int seq_len;
   float* part;  // [bh][chunk][2][D]: sum of k, max |v|
+  float* vinv;  // [bh][D]: 448 / max |v| (1 where the max is 0)
+  float* k_mean;
+  float* v_scale;
 };
 
-// Grid (B*H, kStatChunks): chunk c sums rows c, c + kStatChunks, ... in a fixed order,
-// so the statistics are deterministic.
+// Grid (B*H, kStatChunks): chunk c covers rows [c*S/kStatChunks, (c+1)*S/kStatChunks);
+// each thread reads 16 bytes of a row (D/8 threads per row, kQThreads*8/D rows in flight),
+// the row lanes are then combined in LDS in a fixed order, so the statistics are
+// deterministic.
 template <int D, typename E>
 __global__ __launch_bounds__(kQThreads) void qkv_stats_kernel(StatParams p) {
-  constexpr int kColsPerThread = 2;
-  constexpr int kColThreads = D / kColsPerThread;   // threads across the columns
-  constexpr int kRowLanes = kQThreads / kColThreads;  // rows in flight per step
+  constexpr int kColThreads = D / 8;
+  constexpr int kRowLanes = kQThreads / kColThreads;
+  constexpr int kUnroll = 4;
   __shared__ float red[2][kRowLanes][D];
   const int bh = blockIdx.x;
   const int chunk = blockIdx.y;
@@ -54,19 +59,42 @@ __global__ __launch_bounds__(kQThreads) void qkv_stats_kernel(StatParams p) {
   const uint16_t* vb = p.v + b * p.v_sb + h * p.v_sh;
   const int ct = threadIdx.x % kColThreads;
   const int rl = threadIdx.x / kColThreads;
-  const int d0 = ct * kColsPerThread;
-  float ks[kColsPerThread] = {0.f, 0.f};
-  float vm[kColsPerThread] = {0.f, 0.f};
-  for (int s = chunk + rl * kStatChunks; s < p.seq_len; s += kRowLanes * kStatChunks) {
-    const uint32_t kw = *reinterpret_cast<const uint32_t*>(kb + s * p.k_ss + d0);
-    const uint32_t vw = *reinterpret_cast<const uint32_t*>(vb + s * p.v_ss + d0);
-    ks[0] += E::to_float(static_cast<uint16_t>(kw & 0xffffu));
-    ks[1] += E::to_float(static_cast<uint16_t>(kw >> 16));
-    vm[0] = fmaxf(vm[0], fabsf(E::to_float(static_cast<uint16_t>(vw & 0xffffu))));
-    vm[1] = fmaxf(vm[1], fabsf(E::to_float(static_cast<uint16_t>(vw >> 16))));
+  const int d0 = ct * 8;
+  const int r_begin = static_cast<int>(static_cast<int64_t>(p.seq_len) * chunk / kStatChunks);
+  const int r_end = static_cast<int>(static_cast<int64_t>(p.seq_len) * (chunk + 1) / kStatChunks);
+  float ks[8], vm[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    ks[j] = 0.f;
+    vm[j] = 0.f;
+  }
+  int s = r_begin + rl;
+  for (; s + (kUnroll - 1) * kRowLanes < r_end; s += kUnroll * kRowLanes) {
+    u32x4 kw[kUnroll], vw[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      kw[u] = *reinterpret_cast<const u32x4*>(kb + (s + u * kRowLanes) * p.k_ss + d0);
+      vw[u] = *reinterpret_cast<const u32x4*>(vb + (s + u * kRowLanes) * p.v_ss + d0);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        ks[j] += E::to_float(u16_at(kw[u], j));
+        vm[j] = fmaxf(vm[j], fabsf(E::to_float(u16_at(vw[u], j))));
+      }
+  }
+  for (; s < r_end; s += kRowLanes) {
+    const u32x4 kw = *reinterpret_cast<const u32x4*>(kb + s * p.k_ss + d0);
+    const u32x4 vw = *reinterpret_cast<const u32x4*>(vb + s * p.v_ss + d0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ks[j] += E::to_float(u16_at(kw, j));
+      vm[j] = fmaxf(vm[j], fabsf(E::to_float(u16_at(vw, j))));
+    }
   }
 #pragma unroll
-  for (int j = 0; j < kColsPerThread; ++j) {
+  for (int j = 0; j < 8; ++j) {
     red[0][rl][d0 + j] = ks[j];
     red[1][rl][d0 + j] = vm[j];
   }
@@ -83,6 +111,24 @@ __global__ __launch_bounds__(kQThreads) void qkv_stats_kernel(StatParams p) {
   }
 }
 
+// Grid (B*H): the chunks' partial statistics in a fixed order -> k_mean, v_scale, vinv.
+template <int D>
+__global__ __launch_bounds__(kQThreads) void qkv_stats_finalize_kernel(StatParams p) {
+  const int bh = blockIdx.x;
+  const float* part = p.part + static_cast<int64_t>(bh) * kStatChunks * 2 * D;
+  for (int d = threadIdx.x; d < D; d += kQThreads) {
+    float sum = 0.f, mx = 0.f;
+    for (int c = 0; c < kStatChunks; ++c) {
+      sum += part[c * 2 * D + d];
+      mx = fmaxf(mx, part[c * 2 * D + D + d]);
+    }
+    const int64_t o = static_cast<int64_t>(bh) * D + d;
+    p.k_mean[o] = sum / static_cast<float>(p.seq_len);
+    p.v_scale[o] = mx > 0.f ? mx / 448.f : 1.f;
+    p.vinv[o] = mx > 0.f ? 448.f / mx : 1.f;
+  }
+}
+
 struct QuantParams {
   const uint16_t* q;
   const uint16_t* k;
@@ -94,14 +140,13 @@ struct QuantParams {
   int seq_len;
   int origin;  // first token of the grid (-63..0)
   int s_pad;   // v8t row length: grid tiles * 64
-  const float* part;
+  const float* vinv;     // [bh][D]
+  const float* k_mean_in;  // [bh][D]
   int8_t* q8;
   float* q_scale;  // [bh][ceil((S - origin)/32)]
   int8_t* k8;
   float* k_scale;  // [bh][ceil((S - origin)/64)]
   uint8_t* v8t;
-  float* v_scale;  // [bh][D]
-  float* k_mean;   // [bh][D]
   float* q_kmean;  // [bh][S]
 };
 
@@ -133,21 +178,9 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantParams p) {
   const int wave = tid >> 6;
   const int lane = tid & 63;
 
-  // column statistics of this (b, h), summed over the partial chunks in a fixed order
   for (int d = tid; d < D; d += kQThreads) {
-    const float* part = p.part + static_cast<int64_t>(bh) * kStatChunks * 2 * D;
-    float sum = 0.f, mx = 0.f;
-    for (int c = 0; c < kStatChunks; ++c) {
-      sum += part[c * 2 * D + d];
-      mx = fmaxf(mx, part[c * 2 * D + D + d]);
-    }
-    const float m = sum / static_cast<float>(p.seq_len);
-    mean[d] = m;
-    vinv[d] = mx > 0.f ? 448.f / mx : 1.f;
-    if (tile == 0) {
-      p.k_mean[static_cast<int64_t>(bh) * D + d] = m;
-      p.v_scale[static_cast<int64_t>(bh) * D + d] = mx > 0.f ? mx / 448.f : 1.f;
-    }
+    mean[d] = p.k_mean_in[static_cast<int64_t>(bh) * D + d];
+    vinv[d] = p.vinv[static_cast<int64_t>(bh) * D + d];
   }
   __syncthreads();
 
@@ -258,6 +291,8 @@ template <int D, typename E>
 int launch_quant(const StatParams& sp, const QuantParams& qp, int bhs, hipStream_t st) {
   hipLaunchKernelGGL((qkv_stats_kernel<D, E>), dim3(bhs, kStatChunks), dim3(kQThreads), 0, st, sp);
   MODDIT_CHECK_LAUNCH("quantize_qkv (statistics)");
+  hipLaunchKernelGGL((qkv_stats_finalize_kernel<D>), dim3(bhs), dim3(kQThreads), 0, st, sp);
+  MODDIT_CHECK_LAUNCH("quantize_qkv (statistics, final)");
   hipLaunchKernelGGL((quantize_kernel<D, E>), dim3(bhs, qp.s_pad / 64), dim3(kQThreads), 0, st,
                      qp);
   MODDIT_CHECK_LAUNCH("quantize_qkv");
@@ -311,6 +346,9 @@ extern "C" int moddit_quantize_qkv(const void* q, const void* k, const void* v, 
   sp.heads = heads;
   sp.seq_len = seq_len;
   sp.part = workspace;
+  sp.vinv = workspace + static_cast<int64_t>(batch) * heads * kStatChunks * 2 * head_dim;
+  sp.k_mean = k_mean;
+  sp.v_scale = v_scale;
   QuantParams qp;
   qp.q = static_cast<const uint16_t*>(q);
   qp.k = sp.k;
@@ -322,14 +360,13 @@ extern "C" int moddit_quantize_qkv(const void* q, const void* k, const void* v, 
   qp.seq_len = seq_len;
   qp.origin = grid_origin;
   qp.s_pad = (seq_len - grid_origin + 63) / 64 * 64;
-  qp.part = workspace;
+  qp.vinv = sp.vinv;
+  qp.k_mean_in = k_mean;
   qp.q8 = q8;
   qp.q_scale = q_scale;
   qp.k8 = k8;
   qp.k_scale = k_scale;
   qp.v8t = v8t;
-  qp.v_scale = v_scale;
-  qp.k_mean = k_mean;
   qp.q_kmean = q_kmean;
   const int bhs = batch * heads;
   hipStream_t st = as_stream(stream);
@@ -340,5 +377,5 @@ extern "C" int moddit_quantize_qkv(const void* q, const void* k, const void* v, 
 }
 
 extern "C" int moddit_quantize_workspace_floats(int batch, int heads, int head_dim) {
-  return batch * heads * moddit::kStatChunks * 2 * head_dim;
+  return batch * heads * (moddit::kStatChunks * 2 + 1) * head_dim;
 }
