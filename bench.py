@@ -185,12 +185,15 @@ def _phase(step, W, T):
     return "refresh" if (step - W) % T == T - 1 else "sparse"
 
 
-def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps=50, W=12, T=10):
+def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps=50, W=12, T=10,
+              precision="bf16"):
     """50 steps on one layer: dense warmup, map+fit steps, then sparse steps that each re-run
     the fit, line selection and mask/tiles before the sparse attention, with refreshes
     (dense + map + merge + fit) every T steps. The target sparsity ramps linearly from 50 %
     to 90 % through top_k (one per step, bisected beforehand on the predicted features);
-    per-head sparsity varies with each head's own predicted lines."""
+    per-head sparsity varies with each head's own predicted lines. With precision 'int8'
+    the sparse steps quantise q/k/v and run the int8/fp8 kernel (both timed), as the
+    engine does for create_adaptive_mask_state(precision='int8'); map steps stay bf16."""
     n = art["n"]
     modes = art["modes"]
     x_cur, x_last, smap = art["x_cur"], art["x_last"], art["smap"]
@@ -249,7 +252,10 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
             x_new = ops.solve(ginv, ops.compute_mts(smap, bpf))
             mask, tiles = build(top_k, x_new, x_last)
             e[2].record(stream)
-            ops.block_sparse_fwd(q, k, v, tiles, out=out)
+            if precision == "int8":
+                ops.block_sparse_fwd_q8(ops.quantize_qkv(q, k, v), tiles, out=out)
+            else:
+                ops.block_sparse_fwd(q, k, v, tiles, out=out)
         e3 = torch.cuda.Event(enable_timing=True)
         e3.record(stream)
         e3.synchronize()
@@ -283,7 +289,8 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
         "all_dense_trajectory_ms": round(dense_ms * steps, 2),
         "trajectory_speedup_vs_dense": round(dense_ms * steps / sum(r["ms"] for r in rows), 3),
         "steps": rows,
-        "dtype": "bf16",
+        "dtype": "bf16" if precision == "bf16" else "int8 Q.K^T + fp8 P.V on sparse steps, bf16 elsewhere",
+        "precision": precision,
         "data": "synthetic (seeded structured Q/K/V, same inputs every step)",
     }
 
@@ -378,6 +385,8 @@ def main(argv=None):
     ap.add_argument("--dense-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-q8", action="store_true", help="skip the int8/fp8 path's timings")
+    ap.add_argument("--precision", choices=("bf16", "int8"), default="bf16",
+                    help="--sweep only: arithmetic of the sparse steps (the headline line is bf16)")
     ap.add_argument("--sweep", action="store_true",
                     help="configs[4]: 50-step denoising trajectory (W=12, T=10) with sparsity "
                          "ramping 50%%->90%%; prints its own JSON line")
@@ -387,6 +396,9 @@ def main(argv=None):
                          "prints no JSON")
     args = ap.parse_args(argv)
 
+    if args.precision != "bf16" and not args.sweep:
+        print("--precision applies to --sweep; the headline line is measured in bf16", file=sys.stderr)
+        return 2
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the heads of a layer "
               "shard across GPUs without communication, so the per-GPU figure is the one-GPU "
@@ -436,7 +448,7 @@ def main(argv=None):
 
     if args.sweep:
         result = run_sweep(q, k, v, art, H=H, N=N, D=D, bpf=bpf, bs=bs, union=union,
-                           threshold=args.threshold, config=args.config)
+                           threshold=args.threshold, config=args.config, precision=args.precision)
         print(json.dumps(result), flush=True)
         return 0
 
