@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Headline benchmark: MOD-DiT block-sparse attention on one MI355X.
 
-Workload (the headline): HunyuanVideo-like layer, B=1, H=24,
+Workload (the headline configuration): HunyuanVideo-like layer, B=1, H=24,
 d=128, N=115,200 tokens (30 frames x 48x80), bf16, 64x64 blocks; Q/K synthesized with
 spatial-local + temporal-stripe + heavy-hitter structure from a fixed seed; the mask is
 predicted by the build's own path (dense pass + replay map -> fit -> line selection ->
@@ -174,7 +174,7 @@ def time_events(fn, reps):
 
 
 # ------------------------------------------------------------------------------------
-# configs[4]: denoising-trajectory sweep
+# denoising-trajectory sweep
 # ------------------------------------------------------------------------------------
 def _phase(step, W, T):
     """Schedule of MoD/mod/attn_mask.py:598-712 with the processors' use_dense gate."""
@@ -277,7 +277,7 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
     mean_sparse = sum(r["ms"] for r in sparse_rows) / len(sparse_rows)
     mean_over = sum(r["overhead_ms"] for r in sparse_rows) / len(sparse_rows)
     return {
-        "metric": "configs[4] denoising-trajectory sweep: per-step latency and mask-overhead fraction",
+        "metric": "denoising-trajectory sweep: per-step latency and mask-overhead fraction",
         "config": {"workload": f"{config}-like layer, 50 steps, W={W}, T={T}, sparsity 50%->90%",
                    "H": H, "N": N, "d": D, "block": bs, "tile_rows": "union" if union else "exact"},
         "dense_ms": round(dense_ms, 3),
@@ -388,7 +388,7 @@ def main(argv=None):
     ap.add_argument("--precision", choices=("bf16", "int8"), default="bf16",
                     help="--sweep only: arithmetic of the sparse steps (the headline line is bf16)")
     ap.add_argument("--sweep", action="store_true",
-                    help="configs[4]: 50-step denoising trajectory (W=12, T=10) with sparsity "
+                    help="50-step denoising trajectory (W=12, T=10) with sparsity "
                          "ramping 50%%->90%%; prints its own JSON line")
     ap.add_argument("--profile", choices=("sparse", "dense", "replay", "mask", "copy", "q8"),
                     default=None,

@@ -39,7 +39,7 @@ def _check_attn(out, ref, tag=""):
 
 # ====================================================================== dense attention
 @pytest.mark.parametrize("H,S,D,dtype", [
-    (2, 4096, 64, torch.bfloat16),    # configs[0] plumbing shape
+    (2, 4096, 64, torch.bfloat16),    # the small plumbing shape (B=1, H=2, N=4096, d=64)
     (2, 1000, 128, torch.bfloat16),   # ragged tail (1000 = 7*128 + 104)
     (1, 640, 128, torch.float16),
     (3, 200, 64, torch.float16),
@@ -94,7 +94,7 @@ def test_mask_to_tiles_bit_exact(nb, bs, union):
 
 @pytest.mark.parametrize("union", [False, True])
 def test_block_sparse_config1_matches_masked_fp64(union):
-    # B=1, H=2, N=4096, d=64, 64x64 blocks, 50% random mask, diagonal on
+    # small plumbing shape: B=1, H=2, N=4096, d=64, 64x64 blocks, 50% random mask, diagonal on
     H, S, D, bs = 2, 4096, 64, 64
     q, k, v = (_randn((1, H, S, D), 200 + i, torch.bfloat16) for i in range(3))
     m = _random_block_mask(H, S // bs, 0.5, 5)

@@ -227,7 +227,7 @@ def test_cogvideox_unaligned_text_and_video(tile_rows):
 
 
 def test_configs1_cogvideox_full_shape():
-    """H=48, d=64, 226 text + 13 x 1350 video tokens, bf16
+    """CogVideoX-sized layer: H=48, d=64, 226 text + 13 x 1350 video tokens, bf16
     Q/K/V ~ N(0,1)/sqrt(d), block 64, ~75% mask sparsity. The schedule runs at full shape;
     outputs are checked against fp64 attention under the executed mask for two heads on
     a row subset that covers the text, the first video block and the partial last one."""
@@ -261,7 +261,7 @@ def test_configs1_cogvideox_full_shape():
         qn = _np(q[0, heads])[:, rows]
         kn, vn = _np(k[0, heads]), _np(v[0, heads])
         ref, _ = O.masked_attention(qn, kn, vn, tm, dtype=np.float64)
-        _check_attn(out[0, heads][:, rows], ref, "configs[1] sparse", sparse=True)
+        _check_attn(out[0, heads][:, rows], ref, "cogvideox full-shape sparse", sparse=True)
 
 
 def test_use_dense_and_error_paths():
