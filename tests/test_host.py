@@ -66,6 +66,21 @@ def test_c_abi_rejects_bad_arguments_before_any_launch():
     rc = lib.moddit_mask_from_lines(16, 1, 1, 16, 4, 2, _lib.LAYOUT_WAN, 5, 0, 64, 1,
                                     None, None, None, 0, 0, None)
     assert rc == _lib.MODDIT_EINVAL and b"nb == n" in lib.moddit_last_error()
+    # int8/fp8 path: quantiser grid origin and head_dim, LSE without q . mean_k, query prefix
+    P = 16  # a non-null, 16-byte aligned stand-in pointer (never dereferenced)
+    q8_out = [P] * 9
+    rc = lib.moddit_quantize_qkv(P, P, P, 1, 1, 64, 64, s, s, s, 0, 1, *q8_out, None)
+    assert rc == _lib.MODDIT_EINVAL and b"grid_origin" in lib.moddit_last_error()
+    rc = lib.moddit_quantize_qkv(P, P, P, 1, 1, 64, 96, s, s, s, 0, 0, *q8_out, None)
+    assert rc == _lib.MODDIT_EUNSUPPORTED and b"head_dim" in lib.moddit_last_error()
+    rc = lib.moddit_flash_fwd_q8(P, P, P, P, P, P, None, P, P, 1, 1, 64, 64, s, 0.1, 0, None)
+    assert rc == _lib.MODDIT_EINVAL and b"q_kmean" in lib.moddit_last_error()
+    rc = lib.moddit_block_sparse_fwd_q8(P, P, P, P, P, P, P, P, P, 1, 1, 64, 65, 64, s, 0.1, 0,
+                                        P, P, 1, 1, 0, None)
+    assert rc == _lib.MODDIT_EINVAL and b"q_len" in lib.moddit_last_error()
+    rc = lib.moddit_block_sparse_fwd_q8(P, P, P, P, P, P, P, P, P, 1, 1, 300, 300, 64, s, 0.1, 0,
+                                        P, P, 1, 1, 0, None)
+    assert rc == _lib.MODDIT_EINVAL and b"needs 3" in lib.moddit_last_error()
     with pytest.raises(_lib.ModditError, match="mtm"):
         _lib.check(lib.moddit_mtm_host(-1, 1, 1.0, None), "moddit_mtm_host")
 
