@@ -26,6 +26,7 @@ import torch
 
 import mod_dit_amd as md
 import oracle as O
+from mod_dit_amd import ops
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -278,3 +279,95 @@ def test_hunyuan_processor_padding_mask_and_self_incrementing_step():
         assert not bool(call["pdm"][:, valid:].any())
         ref, sparse = _expected(call, "hunyuan", bs, "exact", video, text, valid=valid)
         _check(call["out"][0], ref, f"hunyuan step {call['step']}", sparse)
+
+
+def _check_q8_call(call, layout, bs, tile_rows, video, valid, tag):
+    """A sparse call of an int8-precision state: video rows against the oracle's model of
+    the int8/fp8 kernel on the same quantised tensors (the quantiser is deterministic),
+    Hunyuan text rows against exact attention (they stay bf16)."""
+    q, k, v = (call[n] for n in ("q", "k", "v"))
+    qn, kn, vn = (_np(t[0]) for t in (q, k, v))
+    H, S = qn.shape[0], qn.shape[1]
+    mask = call["mask"].cpu().numpy()
+    union = tile_rows == "union"
+    qz = ops.quantize_qkv(q, k, v)
+    z = {n: getattr(qz, n)[0].cpu().numpy()
+         for n in ("q8", "q_scale", "k8", "k_scale", "v8t", "v_scale", "k_mean", "q_kmean")}
+    tm = np.zeros((H, S, S), bool)
+    if layout == "hunyuan":
+        _, lists = O.tiles_from_mask(mask[:, :video // bs, :], bs, union, kv_tiles=(valid + 63) // 64)
+        tm[:, :video, :] = O.token_mask_from_tiles(lists, H, video, S)
+    else:
+        _, lists = O.tiles_from_mask(mask, bs, union)
+        tm[:] = O.token_mask_from_tiles(lists, H, S, S)
+    ref_q8, _ = O.attention_q8(z, tm)
+    got = _np(call["out"][0]).astype(np.float64)
+    err = np.abs(got[:, :video] - ref_q8[:, :video])
+    print(f"{tag} int8 video rows: max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
+    assert err.max() <= 4e-3 and err.mean() <= 2e-4, (tag, err.max(), err.mean())
+    if video < S:
+        tt = np.zeros((H, S, S), bool)
+        tt[:, :, :valid] = True
+        ref_t, _ = O.masked_attention(qn, kn, vn, tt, dtype=np.float64)
+        _check(call["out"][0][:, video:], ref_t[:, video:], f"{tag} text rows")
+
+
+@pytest.mark.parametrize("layout", ["wan", "hunyuan"])
+def test_processors_with_int8_precision(layout):
+    """The same call sites with create_adaptive_mask_state(precision='int8'): sparse steps
+    run the quantised kernels (the reference engine's numerics), every other step bf16."""
+    H, D, tpf, bs = 2, 64, 512, 64
+    W, T, top_k, thr = 4, 3, 30, 1e-3
+    rec = Recorder()
+    g = torch.Generator().manual_seed(5)
+    with torch.no_grad():
+        if layout == "wan":
+            F = 3
+            S, C = F * tpf, H * D
+            states = [md.create_adaptive_mask_state("wan", H, S, 0, tpf, F, warmup_steps=W,
+                                                    top_k=top_k, predict_T=T, threshold=thr,
+                                                    block_size=bs, tile_rows="union",
+                                                    precision="int8") for _ in range(2)]
+            attn = MockAttention(C, H, seed=6).to(DEV).to(torch.bfloat16)
+            proc = WanProcessor(states, layer_idx=1, dense_block=1, attention_fn=rec)
+            rot = tuple(t[None, :, None, :].to(DEV) for t in _rotary(S, D))
+            pos = torch.randn(S, C, generator=g)
+            for i in range(W + T):
+                proc.current_step = i
+                for branch in range(2):
+                    x = (torch.randn(1, S, C, generator=g) * 0.5 + pos).to(torch.bfloat16).to(DEV)
+                    proc(attn, x, rot)
+            video, valid = S, S
+        else:
+            F, text, valid_text = 2, 256, 150
+            video = F * tpf
+            S, C, Ce = video + text, H * D, 96
+            st = md.create_adaptive_mask_state("hunyuan", H, video, text, tpf, F, warmup_steps=W,
+                                               top_k=top_k, predict_T=T, threshold=thr,
+                                               block_size=bs, tile_rows="exact", precision="int8")
+            attn = MockAttention(C, H, encoder_dim=Ce, seed=7).to(DEV).to(torch.bfloat16)
+            proc = HunyuanProcessor(st, layer_idx=3, dense_block=1, dense_timestep=1,
+                                    attention_fn=rec)
+            rot = tuple(t.to(DEV) for t in _rotary(video, D))
+            valid = video + valid_text
+            amask = torch.zeros(1, 1, 1, S, dtype=torch.bool, device=DEV)
+            amask[..., :valid] = True
+            pos = torch.randn(video, C, generator=g)
+            for _ in range(W + T):
+                x = (torch.randn(1, video, C, generator=g) * 0.5 + pos).to(torch.bfloat16).to(DEV)
+                e = torch.randn(1, text, Ce, generator=g).to(torch.bfloat16).to(DEV)
+                proc(attn, x, e, amask, rot)
+    n_sparse = 0
+    for call in rec.calls:
+        st = call["state"]
+        phase = "dense" if call["use_dense"] else O.step_phase(call["step"], st["warmup_steps"],
+                                                               st["predict_T"])
+        tag = f"{layout} step {call['step']}"
+        if phase == "sparse":
+            _check_q8_call(call, layout, bs, st["tile_rows"], video, valid, tag)
+            n_sparse += 1
+        else:
+            ref, sparse = _expected(call, layout, bs, st["tile_rows"], video, S - video,
+                                    valid=None if layout == "wan" else valid)
+            _check(call["out"][0], ref, tag, sparse)
+    assert n_sparse >= 2
