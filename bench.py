@@ -298,7 +298,7 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
 # ------------------------------------------------------------------------------------
 # CPU baseline (the oracle's block-sparse attention on a bounded sample)
 # ------------------------------------------------------------------------------------
-def cpu_baseline(q, k, v, tiles, budget_s=12.0):
+def cpu_baseline(q, k, v, tiles, budget_s=12.0, what="the headline layer with the predicted mask"):
     import numpy as np
 
     import oracle as O
@@ -318,19 +318,21 @@ def cpu_baseline(q, k, v, tiles, budget_s=12.0):
     entries = tiles.entries[h].cpu().numpy()
     t0 = time.perf_counter()
     rows = 0
+    org = int(tiles.origin)  # grid row / column 0 is token org (<= 0)
     for t in range(counts.shape[0]):
         ent = entries[t, :counts[t]]
         for half in range(2):
-            r0 = t * 128 + 64 * half
-            if r0 >= N:
+            r0, r1 = max(org + t * 128 + 64 * half, 0), min(org + t * 128 + 64 * half + 64, N)
+            if r0 >= r1:
                 continue
             kts = [int(e >> 2) for e in ent if e & (1 << half)]
             if not kts:
                 continue
-            idx = np.concatenate([np.arange(kt * 64, min(kt * 64 + 64, N)) for kt in kts])
-            O.masked_attention(qh[None, r0:r0 + 64], kh[None, idx], vh[None, idx], None,
+            idx = np.concatenate([np.arange(max(org + kt * 64, 0), min(org + kt * 64 + 64, N))
+                                  for kt in kts])
+            O.masked_attention(qh[None, r0:r1], kh[None, idx], vh[None, idx], None,
                                dtype=np.float32)
-            rows += min(64, N - r0)
+            rows += r1 - r0
         if time.perf_counter() - t0 > budget_s:
             break
     dt = time.perf_counter() - t0
@@ -340,13 +342,101 @@ def cpu_baseline(q, k, v, tiles, budget_s=12.0):
         "unit": "TFLOP/s",
         "cores": int(threads),
         "kind": "port",
-        "sample": f"head 0, first {rows} query rows of the headline layer with the predicted "
-                  f"mask (numpy fp32 oracle, active key blocks only); {dt:.1f} s; effective "
-                  f"(dense-equivalent) FLOPs of the sample / time",
+        "sample": f"head 0, first {rows} query rows of {what} (numpy fp32 oracle, active key "
+                  f"blocks only); {dt:.1f} s; effective (dense-equivalent) FLOPs of the sample / "
+                  f"time",
     }
 
 
 # ------------------------------------------------------------------------------------
+# ------------------------------------------------------------------------------------
+# the two smaller configurations, with random block masks as they are specified
+# ------------------------------------------------------------------------------------
+MASK_CONFIGS = {
+    # plumbing shape: Q/K/V ~ N(0,1), random 50 % block mask with the diagonal forced on
+    "plumbing": dict(H=2, text=0, video=4096, tpf=1024, D=64, density=0.5, qk_scale=1.0),
+    # CogVideoX-v1.5-like: 226 text + 13 x 1350 video tokens, Q/K ~ N(0,1)/sqrt(d), ~75 %
+    # block sparsity with text rows / columns dense, on the shifted grid (text and video
+    # each start on a block boundary)
+    "cogvideox": dict(H=48, text=226, video=13 * 1350, tpf=1350, D=64, density=0.235,
+                      qk_scale=64 ** -0.5),
+}
+
+
+def run_mask_config(name, *, steps, warmup, no_cpu):
+    """Dense and block-sparse attention, mask-prediction overhead and the CPU baseline of a
+    configuration whose mask is random (fixed seed) rather than predicted."""
+    c = MASK_CONFIGS[name]
+    H, text, video, D, bs = c["H"], c["text"], c["video"], c["D"], 64
+    N = text + video
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q, k, v = (torch.randn((1, H, N, D), generator=g, device="cuda") * s
+               for s in (c["qk_scale"], c["qk_scale"], 1.0))
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    if text:
+        tb, vb, origin = md.padded_grid(text, video, bs)
+    else:
+        tb, vb, origin = 0, video // bs, 0
+    nb = tb + vb
+    mask = torch.rand((H, nb, nb), generator=g, device="cuda") < c["density"]
+    mask[:, torch.arange(nb), torch.arange(nb)] = True
+    mask[:, :tb, :] = True
+    mask[:, :, :tb] = True
+    tiles = ops.mask_to_tiles(mask, bs, union_rows=False, grid_origin=origin)
+    pairs = int(tiles.active_tile_pairs().sum().item())
+    sparsity = 1.0 - mask.float().mean().item()
+    eff_flop = 4.0 * H * N * N * D
+    out = torch.empty_like(q)
+    log(f"{name}: H={H} N={N} D={D} grid {nb} blocks (origin {origin}), sparsity {sparsity:.4f}")
+    for _ in range(warmup):
+        ops.block_sparse_fwd(q, k, v, tiles, out=out)
+    ev = time_events(lambda: ops.block_sparse_fwd(q, k, v, tiles, out=out), steps)
+    sparse_ms = sum(ev) / len(ev)
+    dn = time_events(lambda: ops.flash_fwd(q, k, v, return_lse=False, out=out), 3)
+    dense_ms = sorted(dn)[1]
+    # mask prediction at this shape: M^T S + solve + line selection + mask and tile lists
+    bpf = c["tpf"] // bs
+    mt = "cogvideox" if text else "wan"
+    _, smap = md.flash_attn_with_sparsity_map(q, k, v, 1e-4, bs, model_type=mt,
+                                              video_token_num=video, text_token_num=text)
+    smap = smap[0]
+    ginv = md.lstsq.get_inverse(q.device, vb, bpf, 1.0)
+    x0 = ops.solve(ginv, ops.compute_mts(smap, bpf))
+    modes = torch.zeros(H, dtype=torch.uint8, device=q.device)
+    layout = md._lib.LAYOUT_COGVIDEOX if text else md._lib.LAYOUT_WAN
+    top_k = max(1, vb // 4)
+
+    def overhead():
+        x = ops.solve(ginv, ops.compute_mts(smap, bpf))
+        sel = ops.select_lines(x, x0, vb, 10, top_k)
+        ops.mask_from_lines(sel, modes, n=vb, blocks_per_frame=bpf, layout=layout, nb=nb,
+                            text_blocks=tb, block_size=bs, union_rows=False, grid_origin=origin)
+
+    overhead()
+    ov = time_events(overhead, 10)
+    overhead_ms = sorted(ov)[len(ov) // 2]
+    cpu = None if no_cpu else cpu_baseline(q, k, v, tiles, what=f"the {name} layer")
+    exec_flop = 4.0 * D * 64 * 64 * pairs
+    return {
+        "metric": f"block-sparse attn effective TFLOP/s + ms/call, {name} configuration",
+        "value": round(eff_flop / (sparse_ms * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(sparse_ms, 4),
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, random block mask)",
+        "config": {"workload": f"{name}: B=1 H={H} N={N} ({text} text + {video} video) d={D}, "
+                               f"64x64 blocks, tile_rows=exact",
+                   "mask_sparsity": round(sparsity, 5), "grid_origin": origin},
+        "dense_ms": round(dense_ms, 4),
+        "dense_tflops": round(eff_flop / (dense_ms * 1e-3) / 1e12, 3),
+        "executed_tflops": round(exec_flop / (sparse_ms * 1e-3) / 1e12, 3),
+        "speedup_vs_dense": round(dense_ms / sparse_ms, 3),
+        "mask_overhead_ms": round(overhead_ms, 4),
+        "mask_overhead_frac_of_dense": round(overhead_ms / dense_ms, 5),
+        "cpu_baseline": cpu,
+    }
+
+
 def q8_leg(q, k, v, tiles, out, *, ref, eff_flop, reps):
     """Timings of the int8/fp8 path on the same layer and tiles: quantiser, block-sparse and
     dense kernels (HIP events on the launch stream), and the error of its output against
@@ -379,7 +469,9 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", choices=sorted(CONFIGS), default="hunyuan")
+    ap.add_argument("--config", choices=sorted(CONFIGS) + sorted(MASK_CONFIGS), default="hunyuan",
+                    help="hunyuan (headline), wan: structured data, predicted mask; "
+                         "plumbing, cogvideox: random block mask (prints its own JSON line)")
     ap.add_argument("--tile-rows", choices=("union", "exact"), default="exact")
     ap.add_argument("--threshold", type=float, default=1e-4)
     ap.add_argument("--dense-reps", type=int, default=3)
@@ -417,6 +509,12 @@ def main(argv=None):
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"copied {nbytes} bytes x {args.steps}")
+        return 0
+
+    if args.config in MASK_CONFIGS:
+        torch.cuda.set_device(0)
+        print(json.dumps(run_mask_config(args.config, steps=args.steps, warmup=args.warmup,
+                                         no_cpu=args.no_cpu)), flush=True)
         return 0
 
     cfg = CONFIGS[args.config]
