@@ -40,7 +40,6 @@ struct AttnLds {
   static constexpr int kTileBytes = kBN * kRowBytes;      // one 64-key K or V tile
   static constexpr int kTotal = 4 * kTileBytes;           // K ring (2) + V ring (2)
   static constexpr int kChunks = D / 8;                   // 16-byte chunks per row
-  static constexpr int kRowsPerBankCycle = 128 / D;       // rows covering the 64 banks
   static constexpr int kRowsPerWindow = 1024 / kRowBytes; // rows per 1 KB DMA window
   static constexpr int kWindows = kTileBytes / 1024;      // DMA windows per tile
 };
@@ -108,10 +107,6 @@ __device__ __forceinline__ s16x4 lds_read_tr16(const unsigned char* a) {
 // holds two flushes so that a flush never races the next tiles' counts).
 constexpr int kMapFlush = 64;
 constexpr int kMapCountBytes = 4 * 2 * kMapFlush * 4;  // int per (wave, ring slot)
-
-// s_waitcnt with lgkmcnt(0) and vmcnt(n), n < 16 (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
-// lgkmcnt[11:8]); expcnt is left unconstrained.
-#define MODDIT_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(0x0070 | (n))
 
 template <int D, typename E, bool kSparse, bool kRagged, bool kMap = false>
 __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fwd_kernel(AttnParams p) {

@@ -89,8 +89,6 @@ template <int D>
 __device__ __forceinline__ int swz_k8(int r) { return (r / (256 / D)) % (D / 16); }
 __device__ __forceinline__ int swz_v8(int r) { return (r >> 2) & 3; }
 
-#define MODDIT_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(0x0070 | (n))
-
 template <int D, typename E, bool kSparse, bool kRagged>
 __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_q8_kernel(Q8Params p) {
   using L = Q8Lds<D>;

@@ -37,3 +37,8 @@ static __device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
 }
 
 }  // namespace moddit
+
+// s_waitcnt with lgkmcnt(0) and vmcnt(n), n < 16 (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
+// lgkmcnt[11:8]); expcnt is left unconstrained. Used to retire all but the n most recent
+// DMA stages before the barrier that publishes a ring stage.
+#define MODDIT_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(0x0070 | (n))
