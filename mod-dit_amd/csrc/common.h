@@ -121,18 +121,23 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
 }
 
 // ---------------------------------------------------------------------------------
-// Workgroup -> tile mapping that keeps consecutive tiles on one XCD.
-// The dispatcher hands workgroup w to XCD (w % 8); remapping makes XCD x own one
-// contiguous range of logical tiles so tiles that share K/V share that XCD's L2.
+// Workgroup -> tile mapping: runs of kXcdChunk consecutive tiles, dealt to the XCDs in
+// turn. The dispatcher hands workgroup w to XCD (w % 8) whatever the XCDs' progress,
+// so each XCD gets a fixed eighth of the grid. Inside a run, neighbouring query tiles
+// of one head share most K/V tiles in that XCD's L2. Dealing short runs instead of
+// one contiguous eighth per XCD spreads every head over all XCDs: block-sparse heads
+// differ in work by up to 1.6x, and an eighth of a 24-head grid is three whole heads.
+// Tiles past the last whole round of runs keep the dispatcher's order.
 // ---------------------------------------------------------------------------------
 constexpr int kNumXcd = 8;
+constexpr int kXcdChunk = 32;
 
 __device__ __forceinline__ int xcd_remap(int wg, int total) {
+  const int whole = total / (kNumXcd * kXcdChunk) * (kNumXcd * kXcdChunk);
+  if (wg >= whole) return wg;
   const int xcd = wg % kNumXcd;
-  const int local = wg / kNumXcd;
-  const int base = total / kNumXcd;
-  const int rem = total % kNumXcd;
-  return xcd * base + (xcd < rem ? xcd : rem) + local;
+  const int local = wg / kNumXcd;  // position in this XCD's dispatch order
+  return ((local / kXcdChunk) * kNumXcd + xcd) * kXcdChunk + local % kXcdChunk;
 }
 
 }  // namespace moddit

@@ -172,6 +172,54 @@ def test_attention_kernels_are_deterministic():
         assert torch.equal(sp[0], runs[0][1][0])
 
 
+def test_multi_round_grid_writes_every_query_tile():
+    """Workgroups are dealt to the 8 XCDs in runs of 32 tiles; tiles past the last whole
+    round of 256 keep the dispatcher's order. At 5 heads x 128 query tiles (640
+    workgroups: two whole rounds + 128) every output row of the dense, block-sparse,
+    int8/fp8 and replay-map kernels must be written exactly once: outputs start as NaN
+    and none may remain. One row per query tile is checked against fp64 attention."""
+    H, S, D, bs = 5, 16384, 64, 64
+    q, k, v = (_randn((1, H, S, D), 750 + i, torch.bfloat16) for i in range(3))
+    m = _random_block_mask(H, S // bs, 0.3, 37)
+    tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=False)
+    nan_out = lambda: torch.full_like(q, float("nan"))
+    dense = ops.flash_fwd(q, k, v, return_lse=False, out=nan_out())[0]
+    sparse = ops.block_sparse_fwd(q, k, v, tiles, out=nan_out())[0]
+    qz = ops.quantize_qkv(q, k, v)
+    dense8 = ops.flash_fwd_q8(qz, return_lse=False, out=nan_out())[0]
+    sparse8 = ops.block_sparse_fwd_q8(qz, tiles, out=nan_out())[0]
+    for name, o in (("dense", dense), ("sparse", sparse), ("dense q8", dense8),
+                    ("sparse q8", sparse8)):
+        assert not torch.isnan(o).any(), f"{name}: rows left unwritten"
+    # a query tile computed in another tile's place would differ from the bf16 result
+    assert (dense8.float() - dense.float()).abs().mean().item() <= 2e-3
+    assert (sparse8.float() - sparse.float()).abs().mean().item() <= 2e-3
+
+    t = np.arange(S // 128)
+    rows = t * 128 + (t * 53) % 128  # one row per query tile, at varying positions
+    qn, kn, vn = _np(q[0]), _np(k[0]), _np(v[0])
+    ref_d, _ = O.masked_attention(qn[:, rows], kn, vn, None, dtype=np.float64)
+    _check_attn(dense[0][:, rows], ref_d, "multi-round dense")
+    tm = np.repeat(m[:, rows // bs, :], bs, axis=2)  # block mask at the sampled rows
+    ref_s, _ = O.masked_attention(qn[:, rows], kn, vn, tm, dtype=np.float64)
+    _check_attn(sparse[0][:, rows], ref_s, "multi-round block-sparse")
+
+    # replay map through the C-ABI into a NaN-filled map
+    _, lse = ops.flash_fwd(q, k, k)
+    n = S // bs
+    smap = torch.full((1, H, n, n), float("nan"), device=DEV, dtype=torch.float16)
+    st = md._lib.strides3(*q.stride()[:3])
+    rc = md._lib.load().moddit_sparsity_map(
+        q.data_ptr(), k.data_ptr(), lse.data_ptr(), smap.data_ptr(), 1, H, S, D, st, st,
+        D ** -0.5, math.log(1e-3), 0, 0, n, bs, md._lib.BF16,
+        torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    assert not torch.isnan(smap).any(), "replay map: blocks left unwritten"
+    assert torch.equal(smap, ops.sparsity_map(q, k, lse, softmax_scale=D ** -0.5,
+                                              log_threshold=math.log(1e-3), q_video_offset=0,
+                                              k_video_offset=0, video_blocks=n, block_size=bs))
+
+
 # ====================================================================== sparsity map
 def _layout(model_type, bs):
     # tests/test_flash_sparsity.py:22-25
