@@ -60,6 +60,7 @@ struct AttnParams {
   int origin;    // token index of grid row/column 0 (-63..0); see moddit_block_sparse_fwd
   int n_qtiles;
   int n_ktiles;
+  int xcd_run;    // workgroup -> tile order (xcd_remap)
   float scale_log2;  // softmax_scale * log2(e)
   const int32_t* counts;
   const int32_t* entries;
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
   const int half = lane >> 5;
   const int c32 = lane & 31;
 
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = xcd_remap(blockIdx.x, gridDim.x, p.xcd_run);
   const int qt = tile % p.n_qtiles;
   const int bh = tile / p.n_qtiles;
   const int b = bh / p.heads;
@@ -619,6 +620,7 @@ int attention_entry(const void* q, const void* k, const void* v, void* o, float*
   p.origin = origin;
   p.n_qtiles = nq;
   p.n_ktiles = (kv_len - origin + kBN - 1) / kBN;
+  p.xcd_run = xcd_run_for(static_cast<int64_t>(kv_len) * head_dim * 2 * 2);  // K and V
   p.scale_log2 = scale * 1.4426950408889634f;
   p.counts = counts;
   p.entries = entries;

@@ -73,6 +73,7 @@ struct Q8Params {
   int origin;
   int n_qtiles;
   int n_ktiles;
+  int xcd_run;  // workgroup -> tile order (xcd_remap)
   float scale_log2;
   float scale;
   const int32_t* counts;
@@ -109,7 +110,7 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
   const int half = lane >> 5;
   const int c32 = lane & 31;
 
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = xcd_remap(blockIdx.x, gridDim.x, p.xcd_run);
   const int qt = tile % p.n_qtiles;
   const int bh = tile / p.n_qtiles;
   const int h = bh % p.heads;
@@ -544,6 +545,7 @@ int q8_entry(const int8_t* q8, const float* q_scale, const int8_t* k8, const flo
   p.origin = origin;
   p.n_qtiles = nq;
   p.n_ktiles = (seq_len - origin + kBN - 1) / kBN;
+  p.xcd_run = xcd_run_for(static_cast<int64_t>(seq_len) * head_dim * 2);  // int8 K, fp8 V
   p.scale_log2 = scale * 1.4426950408889634f;
   p.scale = scale;
   p.counts = counts;

@@ -49,6 +49,7 @@ struct ReplayParams {
   int valid_k;   // video keys that exist: min(nblk*block, seq_len - k_off)
   int n_qtiles;  // 128-row tiles of the video region
   int n_ktiles;  // 64-key tiles of the video region
+  int xcd_run;   // workgroup -> tile order (xcd_remap)
   float scale;
   float log_thr;
   uint32_t k_bytes;  // byte span of one head's video K rows
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
   const int half = lane >> 5;
   const int c32 = lane & 31;
 
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = xcd_remap(blockIdx.x, gridDim.x, p.xcd_run);
   const int qt = tile % p.n_qtiles;
   const int bh = tile / p.n_qtiles;
   const int b = bh / p.heads;
@@ -303,6 +304,7 @@ extern "C" int moddit_sparsity_map(const void* q, const void* k, const float* ls
   p.valid_k = static_cast<int>(vt < seq_len - k_video_offset ? vt : seq_len - k_video_offset);
   p.n_qtiles = static_cast<int>((vt + kBM - 1) / kBM);
   p.n_ktiles = static_cast<int>(vt / kBN);
+  p.xcd_run = xcd_run_for(vt * head_dim * 2);  // the video K rows a sweep reads
   p.scale = softmax_scale;
   p.log_thr = log_threshold;
   const int64_t k_span = (static_cast<int64_t>(p.valid_k) - 1) * k_strides[2] * 2 + head_dim * 2;

@@ -172,13 +172,18 @@ def test_attention_kernels_are_deterministic():
         assert torch.equal(sp[0], runs[0][1][0])
 
 
-def test_multi_round_grid_writes_every_query_tile():
-    """Workgroups are dealt to the 8 XCDs in runs of 32 tiles; tiles past the last whole
-    round of 256 keep the dispatcher's order. At 5 heads x 128 query tiles (640
-    workgroups: two whole rounds + 128) every output row of the dense, block-sparse,
-    int8/fp8 and replay-map kernels must be written exactly once: outputs start as NaN
-    and none may remain. One row per query tile is checked against fp64 attention."""
-    H, S, D, bs = 5, 16384, 64, 64
+@pytest.mark.parametrize("H,S,D", [
+    (5, 16000, 64),   # 4 MB of K/V per head: one contiguous eighth of 625 tiles per XCD
+    (3, 33024, 128),  # 8.5-17 MB per head: 32-tile runs dealt to the XCDs, 774 tiles =
+                      # three whole rounds of 256 + 6 in the dispatcher's order
+])
+def test_multi_round_grid_writes_every_query_tile(H, S, D):
+    """The workgroup -> tile order (contiguous eighths, or 32-tile runs dealt to the 8
+    XCDs, chosen by the bytes of one head's key sweep) must be a permutation: every
+    output row of the dense, block-sparse, int8/fp8 and replay-map kernels is written
+    (outputs start as NaN and none may remain), and one row per query tile matches fp64
+    attention."""
+    bs = 64
     q, k, v = (_randn((1, H, S, D), 750 + i, torch.bfloat16) for i in range(3))
     m = _random_block_mask(H, S // bs, 0.3, 37)
     tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=False)
