@@ -6,8 +6,11 @@
 // with the operands of the two products at half the width:
 //   S^T (64 keys x 32 queries) = K8 . Q8^T     mfma_i32_32x32x32_i8   (D/32 x 2 per tile)
 //   O^T (D x 32 queries)      += V8^T . P8^T   mfma_f32_32x32x64 fp8  (D/32 per tile)
-// A tile is D bytes per key for K and for V, so the 64 KB of LDS hold a 4-stage ring:
-// K tiles are fetched three tiles ahead, V tiles two.
+// A tile is D bytes per key for K and for V, so a 3-stage ring takes 48 KB of LDS at
+// D=128: K tiles are fetched three tiles ahead, V tiles two, each into the stage its
+// predecessor three tiles back left free at the previous barrier. 48 KB and 166 VGPRs
+// let three workgroups share a CU (three waves per SIMD) in the aligned kernel; the
+// ragged kernel needs 234 VGPRs and runs two.
 //
 // Operand layouts. MFMA products are sums over k, so any assignment of (lane half, byte)
 // to k works as long as both operands use the same one; the layouts below are chosen so
@@ -32,7 +35,7 @@ namespace {
 constexpr int kBM = 128;
 constexpr int kBN = 64;
 constexpr int kThreads = 256;
-constexpr int kStages = 4;
+constexpr int kStages = 3;
 // The row max is moved lazily (when a tile's max exceeds it by more than kRescaleSlack
 // log2 units) and P is formed as exp2(s - m + kPShift): P <= 2^(kPShift + kRescaleSlack)
 // = 2^8.5 stays inside e4m3's range (448) while small probabilities keep kPShift more
@@ -91,7 +94,7 @@ __device__ __forceinline__ int swz_k8(int r) { return (r / (256 / D)) % (D / 16)
 __device__ __forceinline__ int swz_v8(int r) { return (r >> 2) & 3; }
 
 template <int D, typename E, bool kSparse, bool kRagged>
-__global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_q8_kernel(Q8Params p) {
+__global__ __launch_bounds__(kThreads, kRagged ? 2 : 3) __attribute__((amdgpu_waves_per_eu(kRagged ? 2 : 3, kRagged ? 2 : 3))) void attention_q8_kernel(Q8Params p) {
   using L = Q8Lds<D>;
   constexpr int kKSteps = D / 32;                // int8 MFMA k-steps over d
   constexpr int kDSub = D / 32;                  // 32-row blocks of O^T
@@ -361,12 +364,15 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
       bool rescale;
       softmax(s0, s1, kt0, pb, alpha, rescale);
     }
+    __syncthreads();  // K stage 0 is refilled by the first iteration
   }
 
   // Iteration j: S_{j+1} = K_{j+1} Q^T, O += P_j V_j, P_{j+1} = softmax(S_{j+1}); K_{j+3}
-  // and V_{j+2} stream into the stages of K_{j-1} and V_{j-2}.
+  // and V_{j+2} stream into the stages of K_j and V_{j-1}, which the previous iteration
+  // finished reading before its closing barrier (each wave retires its LDS reads first).
   bool pend = false;
   float pend_alpha = 1.f;
+  int st0 = 0, st1 = 1, st2 = 2;  // ring stages of tiles j, j+1, j+2; tile j+3 reuses st0
   for (int j = 0; j < n_iter; ++j) {
     const bool has1 = j + 1 < n_iter;
     const bool has2 = j + 2 < n_iter;
@@ -377,8 +383,8 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
     if (has3) decode(e_n3, kt3, f3);
     int e_n4 = 0;
     if (j + 4 < n_iter) e_n4 = entry(j + 4);
-    if (has3) dma_k(kt3, (j + 3) & 3);
-    if (has2) dma_v(kt2, (j + 2) & 3);
+    if (has3) dma_k(kt3, st0);
+    if (has2) dma_v(kt2, st2);
     __builtin_amdgcn_sched_barrier(0);
 
     if (pend) {
@@ -387,8 +393,8 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
       pend = false;
     }
     const bool act_next = has1 && ((f1 & wbit) != 0);
-    const unsigned char* vs = v_ring + (j & 3) * L::kVTile;
-    const unsigned char* ks1 = k_ring + ((j + 1) & 3) * L::kKTile;
+    const unsigned char* vs = v_ring + st0 * L::kVTile;
+    const unsigned char* ks1 = k_ring + st1 * L::kKTile;
     if (act_cur && act_next) {
       i32x16 s0, s1;
       qk(ks1, s0, s1);
@@ -417,6 +423,10 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
     e_n1 = e_n2;
     e_n2 = e_n3;
     e_n3 = e_n4;
+    const int freed = st0;
+    st0 = st1;
+    st1 = st2;
+    st2 = freed;
   }
   if (pend) {
 #pragma unroll
