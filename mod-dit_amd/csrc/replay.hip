@@ -235,6 +235,10 @@ int launch_replay_impl(const ReplayParams& p, int batch, hipStream_t stream) {
   }
   const int64_t tiles = static_cast<int64_t>(batch) * p.heads * p.n_qtiles;
   if (tiles == 0) return MODDIT_OK;
+  if (tiles > 0x7fffffff) {
+    set_error("sparsity_map: too many tiles (%lld)", static_cast<long long>(tiles));
+    return MODDIT_EINVAL;
+  }
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), L::kTotal,
                      stream, p);
   MODDIT_CHECK_LAUNCH("sparsity_map");
