@@ -350,22 +350,23 @@ def cpu_baseline(q, k, v, tiles, budget_s=12.0, what="the headline layer with th
 
 # ------------------------------------------------------------------------------------
 # ------------------------------------------------------------------------------------
-# the two smaller configurations, with random block masks as they are specified
+# the two smaller configurations, with N(0,1) inputs as they are specified
 # ------------------------------------------------------------------------------------
 MASK_CONFIGS = {
     # plumbing shape: Q/K/V ~ N(0,1), random 50 % block mask with the diagonal forced on
     "plumbing": dict(H=2, text=0, video=4096, tpf=1024, D=64, density=0.5, qk_scale=1.0),
-    # CogVideoX-v1.5-like: 226 text + 13 x 1350 video tokens, Q/K ~ N(0,1)/sqrt(d), ~75 %
-    # block sparsity with text rows / columns dense, on the shifted grid (text and video
-    # each start on a block boundary)
-    "cogvideox": dict(H=48, text=226, video=13 * 1350, tpf=1350, D=64, density=0.235,
+    # CogVideoX-v1.5-like: 226 text + 13 x 1350 video tokens, Q/K ~ N(0,1)/sqrt(d), mask
+    # predicted by this build (map -> fit -> lines) at ~75 % block sparsity, text rows /
+    # columns dense, on the shifted grid (text and video each start on a block boundary)
+    "cogvideox": dict(H=48, text=226, video=13 * 1350, tpf=1350, D=64, sparsity=0.75,
                       qk_scale=64 ** -0.5),
 }
 
 
 def run_mask_config(name, *, steps, warmup, no_cpu):
     """Dense and block-sparse attention, mask-prediction overhead and the CPU baseline of a
-    configuration whose mask is random (fixed seed) rather than predicted."""
+    configuration on seeded N(0,1) inputs: a random block mask (`density`) or one predicted
+    by this build with top_k bisected to a target sparsity (`sparsity`)."""
     c = MASK_CONFIGS[name]
     H, text, video, D, bs = c["H"], c["text"], c["video"], c["D"], 64
     N = text + video
@@ -378,11 +379,45 @@ def run_mask_config(name, *, steps, warmup, no_cpu):
     else:
         tb, vb, origin = 0, video // bs, 0
     nb = tb + vb
-    mask = torch.rand((H, nb, nb), generator=g, device="cuda") < c["density"]
-    mask[:, torch.arange(nb), torch.arange(nb)] = True
-    mask[:, :tb, :] = True
-    mask[:, :, :tb] = True
-    tiles = ops.mask_to_tiles(mask, bs, union_rows=False, grid_origin=origin)
+    # map -> fit at this shape (the predicted mask and the overhead timing both need it)
+    bpf = c["tpf"] // bs
+    mt = "cogvideox" if text else "wan"
+    _, smap = md.flash_attn_with_sparsity_map(q, k, v, 1e-4, bs, model_type=mt,
+                                              video_token_num=video, text_token_num=text)
+    smap = smap[0]
+    ginv = md.lstsq.get_inverse(q.device, vb, bpf, 1.0)
+    x0 = ops.solve(ginv, ops.compute_mts(smap, bpf))
+    x_last = torch.zeros_like(x0)  # features at W-2 are zeros
+    modes = torch.zeros(H, dtype=torch.uint8, device=q.device)
+    layout = md._lib.LAYOUT_COGVIDEOX if text else md._lib.LAYOUT_WAN
+
+    def build(top_k):
+        sel = ops.select_lines(x0, x_last, vb, 10, top_k)
+        return ops.mask_from_lines(sel, modes, n=vb, blocks_per_frame=bpf, layout=layout,
+                                   nb=nb, text_blocks=tb, block_size=bs, union_rows=False,
+                                   grid_origin=origin)
+
+    if "density" in c:
+        mask = torch.rand((H, nb, nb), generator=g, device="cuda") < c["density"]
+        mask[:, torch.arange(nb), torch.arange(nb)] = True
+        mask[:, :tb, :] = True
+        mask[:, :, :tb] = True
+        tiles = ops.mask_to_tiles(mask, bs, union_rows=False, grid_origin=origin)
+        top_k = max(1, vb // 4)
+    else:
+        ops.check_bd(x0, modes, 1.0)
+        lo, hi, best = 1, 3 * vb - 1, None
+        while lo <= hi:  # top_k whose mask sparsity is closest to the target
+            mid = (lo + hi) // 2
+            sp = 1.0 - build(mid)[0].float().mean().item()
+            if best is None or abs(sp - c["sparsity"]) < abs(best[1] - c["sparsity"]):
+                best = (mid, sp)
+            if sp > c["sparsity"]:
+                lo = mid + 1
+            else:
+                hi = mid - 1
+        top_k = best[0]
+        mask, tiles = build(top_k)
     pairs = int(tiles.active_tile_pairs().sum().item())
     sparsity = 1.0 - mask.float().mean().item()
     eff_flop = 4.0 * H * N * N * D
@@ -394,18 +429,8 @@ def run_mask_config(name, *, steps, warmup, no_cpu):
     sparse_ms = sum(ev) / len(ev)
     dn = time_events(lambda: ops.flash_fwd(q, k, v, return_lse=False, out=out), 3)
     dense_ms = sorted(dn)[1]
-    # mask prediction at this shape: M^T S + solve + line selection + mask and tile lists
-    bpf = c["tpf"] // bs
-    mt = "cogvideox" if text else "wan"
-    _, smap = md.flash_attn_with_sparsity_map(q, k, v, 1e-4, bs, model_type=mt,
-                                              video_token_num=video, text_token_num=text)
-    smap = smap[0]
-    ginv = md.lstsq.get_inverse(q.device, vb, bpf, 1.0)
-    x0 = ops.solve(ginv, ops.compute_mts(smap, bpf))
-    modes = torch.zeros(H, dtype=torch.uint8, device=q.device)
-    layout = md._lib.LAYOUT_COGVIDEOX if text else md._lib.LAYOUT_WAN
-    top_k = max(1, vb // 4)
 
+    # mask prediction per step: M^T S + solve + line selection + mask and tile lists
     def overhead():
         x = ops.solve(ginv, ops.compute_mts(smap, bpf))
         sel = ops.select_lines(x, x0, vb, 10, top_k)
@@ -423,10 +448,12 @@ def run_mask_config(name, *, steps, warmup, no_cpu):
         "unit": "TFLOP/s",
         "ms_per_step": round(sparse_ms, 4),
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) Q/K/V, random block mask)",
+        "data": ("synthetic (seeded N(0,1) Q/K/V, random block mask)" if "density" in c else
+                 "synthetic (seeded N(0,1) Q/K/V; mask predicted by this build)"),
         "config": {"workload": f"{name}: B=1 H={H} N={N} ({text} text + {video} video) d={D}, "
                                f"64x64 blocks, tile_rows=exact",
-                   "mask_sparsity": round(sparsity, 5), "grid_origin": origin},
+                   "mask_sparsity": round(sparsity, 5), "grid_origin": origin,
+                   "top_k": top_k if "density" not in c else None},
         "dense_ms": round(dense_ms, 4),
         "dense_tflops": round(eff_flop / (dense_ms * 1e-3) / 1e12, 3),
         "executed_tflops": round(exec_flop / (sparse_ms * 1e-3) / 1e12, 3),
@@ -471,7 +498,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", choices=sorted(CONFIGS) + sorted(MASK_CONFIGS), default="hunyuan",
                     help="hunyuan (headline), wan: structured data, predicted mask; "
-                         "plumbing, cogvideox: random block mask (prints its own JSON line)")
+                         "plumbing: random block mask, cogvideox: mask predicted on N(0,1) inputs "
+                         "(both print their own JSON line)")
     ap.add_argument("--tile-rows", choices=("union", "exact"), default="exact")
     ap.add_argument("--threshold", type=float, default=1e-4)
     ap.add_argument("--dense-reps", type=int, default=3)
