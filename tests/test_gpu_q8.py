@@ -250,3 +250,45 @@ def test_schedule_int8_precision_cogvideox_shifted_grid():
     assert checked == 2
     with pytest.raises(ValueError, match="precision"):
         md.create_adaptive_mask_state("wan", 2, 1024, 0, 512, 2, precision="fp8")
+
+
+def test_short_tile_lists_bf16_and_int8():
+    """Query tiles with 0..5 active key tiles: every prologue / prefetch / ring-wait branch
+    of both attention kernels (the int8/fp8 ring keeps K three tiles ahead and V two, the
+    bf16 ring one), with random row bits, against the oracle (bf16: fp64 attention, the
+    north-star bound; int8/fp8: the quantised model, 4e-3 / 2e-4); rows without keys
+    give zeros and an LSE of -inf."""
+    H, S, D, bs = 2, 1536, 128, 64
+    nb = S // bs
+    q, k, v = (_randn((1, H, S, D), 60 + i, torch.bfloat16) for i in range(3))
+    rng = np.random.default_rng(17)
+    m = np.zeros((H, nb, nb), dtype=bool)
+    want = np.zeros((H, nb // 2), dtype=np.int32)
+    for h in range(H):
+        for t in range(nb // 2):
+            cnt = (t + 3 * h) % 6
+            want[h, t] = cnt
+            for kt in rng.choice(nb, size=cnt, replace=False):
+                bits = int(rng.integers(1, 4))
+                m[h, 2 * t, kt] = bool(bits & 1)
+                m[h, 2 * t + 1, kt] = bool(bits & 2)
+    tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=False)
+    assert np.array_equal(tiles.counts.cpu().numpy(), want)
+    c = tiles.counts.cpu().numpy()
+    e = tiles.entries.cpu().numpy()
+    lists = [[[int(x) for x in e[h, t, :c[h, t]]] for t in range(c.shape[1])] for h in range(H)]
+    tm = O.token_mask_from_tiles(lists, H, S, S)
+    empty = ~tm.any(axis=-1)  # (H, S) rows without keys
+
+    out, lse = ops.block_sparse_fwd(q, k, v, tiles, return_lse=True)
+    ref, ref_lse = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), tm, dtype=np.float64)
+    _check(out[0], ref, "bf16 short lists", 2e-2, 2e-3)
+    _check_lse(lse[0], ref_lse, "bf16 short lists", 2e-3)
+    assert torch.all(out[0][torch.from_numpy(empty).to(DEV)] == 0)
+
+    qz = ops.quantize_qkv(q, k, v)
+    out8, lse8 = ops.block_sparse_fwd_q8(qz, tiles, return_lse=True)
+    ref8, ref8_lse = O.attention_q8(_z_np(qz), tm)
+    _check(out8[0], ref8, "int8/fp8 short lists", 4e-3, 2e-4)
+    _check_lse(lse8[0], ref8_lse, "int8/fp8 short lists", 2e-4)
+    assert torch.all(out8[0][torch.from_numpy(empty).to(DEV)] == 0)
