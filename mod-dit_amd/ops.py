@@ -98,15 +98,17 @@ def _attention(q, k, v, scale, return_lse, tiles: TileList | None, out=None):
     lse = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32) if return_lse else None
     if scale is None:
         scale = D ** -0.5
+    if tiles is not None and tiles.counts.shape[0] != H:
+        raise ValueError(f"tile lists cover {tiles.counts.shape[0]} heads, attention has {H}")
     lib = _lib.load()
+    if out.numel() == 0:
+        return out, lse  # no query rows: nothing to compute (empty tensors have no storage)
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), _ptr(lse), B, H, Sq, Skv, D,
             strides3(*q.stride()[:3]), strides3(*k.stride()[:3]), strides3(*v.stride()[:3]),
             strides3(*out.stride()[:3]), float(scale), dt)
     if tiles is None:
         check(lib.moddit_flash_fwd(*args, _stream(q)), "moddit_flash_fwd")
     else:
-        if tiles.counts.shape[0] != H:
-            raise ValueError(f"tile lists cover {tiles.counts.shape[0]} heads, attention has {H}")
         check(lib.moddit_block_sparse_fwd(*args, tiles.counts.data_ptr(), tiles.entries.data_ptr(),
                                           tiles.n_qtiles, tiles.cap, int(tiles.origin), _stream(q)),
               "moddit_block_sparse_fwd")
@@ -205,6 +207,8 @@ def quantize_qkv(q, k, v, grid_origin: int = 0) -> QuantizedQKV:
         k_mean=torch.empty((B, H, D), device=dev, dtype=torch.float32),
         q_kmean=torch.empty((B, H, S), device=dev, dtype=torch.float32),
         dtype=q.dtype, origin=int(grid_origin))
+    if B * H * S == 0:
+        return out  # no rows to quantise
     check(lib.moddit_quantize_qkv(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), B, H, S, D, strides3(*q.stride()[:3]),
         strides3(*k.stride()[:3]), strides3(*v.stride()[:3]), dt, int(grid_origin),
@@ -234,6 +238,10 @@ def _attention_q8(qz: QuantizedQKV, scale, return_lse, tiles: TileList | None, o
     if qz.origin != origin:
         raise ValueError(f"q/k/v were quantised on the grid starting at {qz.origin}, the "
                          f"attention runs on the grid starting at {origin}")
+    if tiles is not None and tiles.counts.shape[0] != H:
+        raise ValueError(f"tile lists cover {tiles.counts.shape[0]} heads, attention has {H}")
+    if out.numel() == 0:
+        return out, lse  # no query rows
     head = (qz.q8.data_ptr(), qz.q_scale.data_ptr(), qz.k8.data_ptr(), qz.k_scale.data_ptr(),
             qz.v8t.data_ptr(), qz.v_scale.data_ptr(), qz.q_kmean.data_ptr(), out.data_ptr(),
             _ptr(lse), B, H, S)
@@ -241,8 +249,6 @@ def _attention_q8(qz: QuantizedQKV, scale, return_lse, tiles: TileList | None, o
     if tiles is None:
         check(lib.moddit_flash_fwd_q8(*head, *tail, _stream(out)), "moddit_flash_fwd_q8")
     else:
-        if tiles.counts.shape[0] != H:
-            raise ValueError(f"tile lists cover {tiles.counts.shape[0]} heads, attention has {H}")
         check(lib.moddit_block_sparse_fwd_q8(*head, q_len, *tail, tiles.counts.data_ptr(),
                                              tiles.entries.data_ptr(), tiles.n_qtiles, tiles.cap,
                                              origin, _stream(out)),

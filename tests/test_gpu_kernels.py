@@ -504,3 +504,39 @@ def test_refresh_merge_exact():
     mask = torch.from_numpy(full).to(DEV)[:, :n, :n]  # strided view like the hunyuan slice
     got = ops.refresh_merge(torch.from_numpy(prev).to(DEV), torch.from_numpy(cur).to(DEV), mask)
     assert np.array_equal(got.cpu().numpy(), O.refresh_merge(prev, cur, full[:, :n, :n]))
+
+
+@pytest.mark.parametrize("S", [0, 1, 17, 63, 64, 65, 127, 129])
+def test_tiny_and_ragged_sequences(S):
+    """Sequences shorter than one 64-key tile or one 128-row query tile, and one token past
+    a tile boundary: dense, block-sparse (every block active) and int8/fp8 dense attention
+    against the oracle; an empty sequence gives empty outputs."""
+    H, D, bs = 2, 128, 64
+    q, k, v = (_randn((1, H, S, D), 910 + i, torch.bfloat16) for i in range(3))
+    out, lse = ops.flash_fwd(q, k, v)
+    nb = max(1, -(-S // bs))
+    tiles = ops.mask_to_tiles(torch.ones((H, nb, nb), dtype=torch.bool, device=DEV), bs,
+                              union_rows=False)
+    sp, sp_lse = ops.block_sparse_fwd(q, k, v, tiles, return_lse=True)
+    qz = ops.quantize_qkv(q, k, v)
+    o8, l8 = ops.flash_fwd_q8(qz)
+    for t_, shape in ((out, (1, H, S, D)), (lse, (1, H, S)), (sp, (1, H, S, D)),
+                      (o8, (1, H, S, D)), (l8, (1, H, S))):
+        assert tuple(t_.shape) == shape
+    if S == 0:
+        return
+    qn, kn, vn = _np(q[0]), _np(k[0]), _np(v[0])
+    ref, ref_lse = O.masked_attention(qn, kn, vn, None, dtype=np.float64)
+    _check_attn(out[0], ref, f"dense S={S}")
+    _check_attn(sp[0], ref, f"block-sparse S={S}")
+    np.testing.assert_allclose(_np(lse[0]), ref_lse, rtol=0, atol=2e-3)
+    np.testing.assert_allclose(_np(sp_lse[0]), ref_lse, rtol=0, atol=2e-3)
+    z = {name: getattr(qz, name)[0].cpu().numpy()
+         for name in ("q8", "q_scale", "k8", "k_scale", "v8t", "v_scale", "k_mean", "q_kmean")}
+    ref8, ref8_lse = O.attention_q8(z)
+    # a row over few keys keeps |o| ~ |v|: the bf16 rounding of the output (2^-9 relative)
+    # then dominates the kernel-vs-model difference, so it is allowed on top of 4e-3
+    err = np.abs(_np(o8[0]).astype(np.float64) - ref8)
+    print(f"int8/fp8 dense S={S}: max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
+    assert np.all(err <= 4e-3 + 2.0 ** -8 * np.abs(ref8)) and err.mean() <= 2e-3
+    np.testing.assert_allclose(_np(l8[0]), ref8_lse, rtol=0, atol=2e-4)
