@@ -540,3 +540,25 @@ def test_tiny_and_ragged_sequences(S):
     print(f"int8/fp8 dense S={S}: max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
     assert np.all(err <= 4e-3 + 2.0 ** -8 * np.abs(ref8)) and err.mean() <= 2e-3
     np.testing.assert_allclose(_np(l8[0]), ref8_lse, rtol=0, atol=2e-4)
+
+
+def test_diagonal_block_mask_is_per_block_attention():
+    """A mask holding only the diagonal 64x64 blocks equals attention inside each block on
+    its own (computed block by block with the oracle), for the bf16 kernel in exact and
+    union rows; union rows add the partner block of each 128-row tile."""
+    H, S, D, bs = 2, 640, 128, 64
+    nb = S // bs
+    q, k, v = (_randn((1, H, S, D), 950 + i, torch.bfloat16) for i in range(3))
+    m = np.zeros((H, nb, nb), dtype=bool)
+    m[:, np.arange(nb), np.arange(nb)] = True
+    qn, kn, vn = _np(q[0]), _np(k[0]), _np(v[0])
+    for union in (False, True):
+        tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=union)
+        out, _ = ops.block_sparse_fwd(q, k, v, tiles)
+        span = 2 * bs if union else bs  # keys a row sees: its block, or its 128-row tile
+        ref = np.zeros((H, S, D))
+        for b0 in range(0, S, span):
+            sl = slice(b0, b0 + span)
+            ref[:, sl], _ = O.masked_attention(qn[:, sl], kn[:, sl], vn[:, sl], None,
+                                               dtype=np.float64)
+        _check_attn(out[0], ref, f"diagonal mask union={union}")
