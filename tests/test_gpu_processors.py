@@ -14,6 +14,12 @@ reference call sites around `SparseAttentionWithMap`:
   streams are concatenated, dense steps use SDPA with the padding mask, sparse steps
   pass `pre_defined_mask = attention_mask[0, 0].expand(S, S)`, and the processor
   increments its own `current_step` after every call (:181).
+- CogVideoX (MoD/models/cogvideox/attention_processor.py:89-240): text first, one QKV
+  projection for the joint sequence, QK norm over the head dimension, rotary embedding
+  on the video tokens only, the `use_dense` gate evaluated by the processor (SDPA when
+  it holds), otherwise one `SparseAttentionWithMap` call per batch element with that
+  element's state and no `use_dense` argument; unaligned text and video lengths run on
+  the shifted block grid.
 
 Every attention call is checked against fp64 attention under the mask the state held
 for that call, and the two CFG states are checked to evolve
@@ -45,15 +51,16 @@ def _check(out, ref, tag, sparse=False):
 class MockAttention(torch.nn.Module):
     """The parts of diffusers' Attention the processors touch."""
 
-    def __init__(self, dim, heads, encoder_dim=None, seed=0):
+    def __init__(self, dim, heads, encoder_dim=None, seed=0, norm_dim=None):
         super().__init__()
         torch.manual_seed(seed)
         self.heads = heads
+        self.is_cross_attention = False
         self.to_q = torch.nn.Linear(dim, dim)
         self.to_k = torch.nn.Linear(dim, dim)
         self.to_v = torch.nn.Linear(dim, dim)
-        self.norm_q = torch.nn.RMSNorm(dim, eps=1e-6)
-        self.norm_k = torch.nn.RMSNorm(dim, eps=1e-6)
+        self.norm_q = torch.nn.RMSNorm(norm_dim or dim, eps=1e-6)
+        self.norm_k = torch.nn.RMSNorm(norm_dim or dim, eps=1e-6)
         self.to_out = torch.nn.ModuleList([torch.nn.Linear(dim, dim), torch.nn.Dropout(0.0)])
         if encoder_dim is not None:
             self.add_q_proj = torch.nn.Linear(encoder_dim, dim)
@@ -180,6 +187,61 @@ class HunyuanProcessor:
         return hidden, enc
 
 
+class CogVideoXProcessor:
+    """Restatement of the CogVideoX call site (attention_processor.py:89-240)."""
+
+    def __init__(self, warmup_state, layer_idx, dense_block, dense_timestep, attention_fn):
+        self.warmup_state = warmup_state  # one state per batch element
+        self.layer_idx = layer_idx
+        self.dense_block = dense_block
+        self.dense_timestep = dense_timestep
+        self.attention_fn = attention_fn
+        self.dense_outputs = []
+
+    def __call__(self, attn, hidden_states, encoder_hidden_states, rotary_emb, timestep,
+                 numeral_timestep):
+        text_seq_length = encoder_hidden_states.size(1)
+        hidden_states = torch.cat([encoder_hidden_states, hidden_states], dim=1)
+        batch_size = hidden_states.shape[0]
+        query = attn.to_q(hidden_states)
+        key = attn.to_k(hidden_states)
+        value = attn.to_v(hidden_states)
+        head_dim = key.shape[-1] // attn.heads
+        query = query.view(batch_size, -1, attn.heads, head_dim).transpose(1, 2)
+        key = key.view(batch_size, -1, attn.heads, head_dim).transpose(1, 2)
+        value = value.view(batch_size, -1, attn.heads, head_dim).transpose(1, 2)
+        query = attn.norm_q(query)
+        key = attn.norm_k(key)
+        query[:, :, text_seq_length:] = _apply_rotary_interleaved(query[:, :, text_seq_length:],
+                                                                  *rotary_emb)
+        if not attn.is_cross_attention:
+            key[:, :, text_seq_length:] = _apply_rotary_interleaved(key[:, :, text_seq_length:],
+                                                                    *rotary_emb)
+        use_dense = (timestep is None or numeral_timestep < self.dense_timestep
+                     or self.layer_idx < self.dense_block or self.warmup_state is None
+                     or numeral_timestep < self.warmup_state[0]["warmup_steps"] - 2)
+        if use_dense:
+            hidden = torch.nn.functional.scaled_dot_product_attention(
+                query.float(), key.float(), value.float(), dropout_p=0.0,
+                is_causal=False).to(query.dtype)
+            self.dense_outputs.append(hidden)
+        else:
+            parts = []
+            for i in range(batch_size):
+                h_i, _ = self.attention_fn(query=query[i].unsqueeze(0), key=key[i].unsqueeze(0),
+                                           value=value[i].unsqueeze(0), logger=None,
+                                           warmup_state=self.warmup_state[i],
+                                           current_step=int(numeral_timestep),
+                                           layer_idx=self.layer_idx)
+                parts.append(h_i)
+            hidden = torch.cat(parts, dim=0)
+        hidden = hidden.transpose(1, 2).reshape(batch_size, -1, attn.heads * head_dim)
+        hidden = attn.to_out[1](attn.to_out[0](hidden.to(query.dtype)))
+        encoder_out, video_out = hidden.split([text_seq_length, hidden.size(1) - text_seq_length],
+                                              dim=1)
+        return video_out, encoder_out
+
+
 def _expected(call, layout, bs, tile_rows, video, text, valid=None):
     """fp64 attention of one recorded call under the mask its state held."""
     q, k, v = (_np(call[n][0]) for n in ("q", "k", "v"))
@@ -202,6 +264,11 @@ def _expected(call, layout, bs, tile_rows, video, text, valid=None):
         tm = np.zeros((H, S, S), bool)
         tm[:, :video, :] = O.token_mask_from_tiles(lists, H, video, S)
         tm[:, video:, :valid] = True
+    elif layout == "cogvideox":
+        _, _, origin = O.cogvideox_grid(text, video, bs)
+        _, lists = O.tiles_from_mask(mask, bs, union)
+        tm = O.token_mask_from_tiles(lists, H, S, S, origin=origin)
+        assert tm[:, :text, :].all() and tm[:, :, :text].all()  # text rows/cols are dense
     else:
         _, lists = O.tiles_from_mask(mask, bs, union)
         tm = O.token_mask_from_tiles(lists, H, S, S)
@@ -371,3 +438,42 @@ def test_processors_with_int8_precision(layout):
                                     valid=None if layout == "wan" else valid)
             _check(call["out"][0], ref, tag, sparse)
     assert n_sparse >= 2
+
+
+@pytest.mark.parametrize("tile_rows", ["exact", "union"])
+def test_cogvideox_processor_per_sample_states_and_shifted_grid(tile_rows):
+    H, D, F, tpf, bs, B = 2, 64, 3, 150, 64, 2
+    text, video = 50, F * tpf  # neither block-aligned: the grid starts 14 tokens early
+    S, C = text + video, H * D
+    W, T, top_k, thr, steps = 4, 3, 6, 1e-3, 10
+    states = [md.create_adaptive_mask_state("cogvideox", H, video, text, tpf, F, warmup_steps=W,
+                                            top_k=top_k, predict_T=T, threshold=thr,
+                                            block_size=bs, tile_rows=tile_rows)
+              for _ in range(B)]
+    attn = MockAttention(C, H, seed=5, norm_dim=D).to(DEV).to(torch.bfloat16)
+    rec = Recorder()
+    procs = [CogVideoXProcessor(states, layer_idx=li, dense_block=1, dense_timestep=0,
+                                attention_fn=rec) for li in range(2)]
+    rot = tuple(t[None, None].to(DEV) for t in _rotary(video, D))  # (1, 1, Sv, D)
+    g = torch.Generator().manual_seed(6)
+    pos = torch.randn(video, C, generator=g)
+    with torch.no_grad():
+        for i in range(steps):
+            x = (torch.randn(B, video, C, generator=g) * 0.5 + pos).to(torch.bfloat16).to(DEV)
+            e = torch.randn(B, text, C, generator=g).to(torch.bfloat16).to(DEV)
+            for p in procs:
+                out, enc = p(attn, x, e, rot, timestep=torch.tensor([999 - i]),
+                             numeral_timestep=i)
+                assert out.shape == (B, video, C) and enc.shape == (B, text, C)
+    # layer 0 is a dense block; layer 1 takes SDPA for steps < W-2, then one call per sample
+    assert len(procs[0].dense_outputs) == steps and len(procs[1].dense_outputs) == W - 2
+    assert len(rec.calls) == (steps - (W - 2)) * B
+    for n, call in enumerate(rec.calls):
+        step, sample = W - 2 + n // B, n % B
+        assert call["step"] == step and call["state"] is states[sample]
+        assert not call["use_dense"]
+        ref, sparse = _expected(call, "cogvideox", bs, tile_rows, video, text)
+        _check(call["out"][0], ref, f"cogvideox step {step} sample {sample}", sparse)
+    assert states[0]["mask"] is not None and states[1]["mask"] is not None
+    f0, f1 = (st["features_history"][-1]["_x"] for st in states)
+    assert not torch.equal(f0, f1)
