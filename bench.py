@@ -464,9 +464,13 @@ def run_mask_config(name, *, steps, warmup, no_cpu):
     }
 
 
-def q8_leg(q, k, v, tiles, out, *, ref, eff_flop, reps):
+INT8_FP8_PEAK_TFLOPS = 5000.0  # MI355X dense int8 / fp8 MFMA peak
+
+
+def q8_leg(q, k, v, tiles, out, *, ref, eff_flop, exec_flop, reps):
     """Timings of the int8/fp8 path on the same layer and tiles: quantiser, block-sparse and
-    dense kernels (HIP events on the launch stream), and the error of its output against
+    dense kernels (HIP events on the launch stream), the block-sparse kernel's executed
+    rate against the 5.0 POP/s int8/fp8 MFMA peak, and the error of its output against
     the bf16 kernel's (`ref`)."""
     qz = ops.quantize_qkv(q, k, v)
     ops.block_sparse_fwd_q8(qz, tiles, out=out)
@@ -483,6 +487,9 @@ def q8_leg(q, k, v, tiles, out, *, ref, eff_flop, reps):
         "quantize_ms": round(quant_ms, 3),
         "sparse_ms": round(sparse_ms, 3),
         "sparse_eff_tflops": round(eff_flop / (sparse_ms * 1e-3) / 1e12, 3),
+        "sparse_executed_tflops": round(exec_flop / (sparse_ms * 1e-3) / 1e12, 3),
+        "sparse_frac_of_int8_fp8_peak": round(exec_flop / (sparse_ms * 1e-3) / 1e12
+                                              / INT8_FP8_PEAK_TFLOPS, 4),
         "sparse_incl_quantize_ms": round(sparse_ms + quant_ms, 3),
         "dense_ms": round(dense_ms, 3),
         "dense_tflops": round(eff_flop / (dense_ms * 1e-3) / 1e12, 3),
@@ -642,7 +649,8 @@ def main(argv=None):
     q8 = None
     if not args.no_q8:
         log("timing the int8/fp8 path")
-        q8 = q8_leg(q, k, v, tiles, out, ref=out.clone(), eff_flop=eff_flop, reps=args.steps)
+        q8 = q8_leg(q, k, v, tiles, out, ref=out.clone(), eff_flop=eff_flop, exec_flop=exec_flop,
+                    reps=args.steps)
 
     cpu = None
     if not args.no_cpu:
