@@ -137,9 +137,7 @@ def predict_tiles(q, k, v, *, block_size, bpf, threshold, target_sparsity, union
 def mask_overhead_once(art, *, bpf, block_size, union):
     """One refresh-step mask pipeline: M^T S, solve, select, mask + tiles."""
     n = art["n"]
-    mts = ops.compute_mts(art["smap"], bpf)
-    ginv = md.lstsq.get_inverse(mts.device, n, bpf, 1.0)
-    x = ops.solve(ginv, mts)
+    x = md.lstsq.fit(ops.compute_mts(art["smap"], bpf), n, bpf, 1.0)
     sel = ops.select_lines(x, art["x_cur"], n, art["T"], art["top_k"])
     ops.mask_from_lines(sel, art["modes"], n=n, blocks_per_frame=bpf, layout=md._lib.LAYOUT_WAN,
                         nb=n, text_blocks=0, block_size=block_size, union_rows=union)
@@ -197,8 +195,6 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
     n = art["n"]
     modes = art["modes"]
     x_cur, x_last, smap = art["x_cur"], art["x_last"], art["smap"]
-    ginv = md.lstsq.get_inverse(q.device, n, bpf, 1.0)
-
     def build(top_k, xc, xl):
         sel = ops.select_lines(xc, xl, n, T, top_k)
         return ops.mask_from_lines(sel, modes, n=n, blocks_per_frame=bpf, layout=md._lib.LAYOUT_WAN,
@@ -242,14 +238,14 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
                 cur_map = ops.refresh_merge(smap, cur_map, mask)
             e[1].record(stream)
             if ph != "map_fit":
-                x_new = ops.solve(ginv, ops.compute_mts(cur_map, bpf))
+                x_new = md.lstsq.fit(ops.compute_mts(cur_map, bpf), n, bpf, 1.0)
                 x_last, x_cur = x_cur, x_new
                 mask, tiles = build(top_k, x_cur, x_last)
             smap = cur_map
             e[2].record(stream)
         else:
             e[1].record(stream)
-            x_new = ops.solve(ginv, ops.compute_mts(smap, bpf))
+            x_new = md.lstsq.fit(ops.compute_mts(smap, bpf), n, bpf, 1.0)
             mask, tiles = build(top_k, x_new, x_last)
             e[2].record(stream)
             if precision == "int8":
@@ -385,8 +381,7 @@ def run_mask_config(name, *, steps, warmup, no_cpu):
     _, smap = md.flash_attn_with_sparsity_map(q, k, v, 1e-4, bs, model_type=mt,
                                               video_token_num=video, text_token_num=text)
     smap = smap[0]
-    ginv = md.lstsq.get_inverse(q.device, vb, bpf, 1.0)
-    x0 = ops.solve(ginv, ops.compute_mts(smap, bpf))
+    x0 = md.lstsq.fit(ops.compute_mts(smap, bpf), vb, bpf, 1.0)
     x_last = torch.zeros_like(x0)  # features at W-2 are zeros
     modes = torch.zeros(H, dtype=torch.uint8, device=q.device)
     layout = md._lib.LAYOUT_COGVIDEOX if text else md._lib.LAYOUT_WAN
@@ -432,7 +427,7 @@ def run_mask_config(name, *, steps, warmup, no_cpu):
 
     # mask prediction per step: M^T S + solve + line selection + mask and tile lists
     def overhead():
-        x = ops.solve(ginv, ops.compute_mts(smap, bpf))
+        x = md.lstsq.fit(ops.compute_mts(smap, bpf), vb, bpf, 1.0)
         sel = ops.select_lines(x, x0, vb, 10, top_k)
         ops.mask_from_lines(sel, modes, n=vb, blocks_per_frame=bpf, layout=layout, nb=nb,
                             text_blocks=tb, block_size=bs, union_rows=False, grid_origin=origin)

@@ -204,12 +204,26 @@ int moddit_mts(const void* map, int map_dtype, int heads, int n, int blocks_per_
 int moddit_mtm_host(int n, int blocks_per_frame, double regularization, double* mtm_out);
 
 /*
- * X[h,:] = Ginv . mts[h,:] for all heads: ginv (F,F) fp32 row-major (symmetric inverse of
- * M^T M + lambda*I), mts (H,F), x (H,F).
- * Replaces _solve_all_heads (MoD/mod/cuda_lstsq.py:189-208).
+ * Ridge fit of the line model, X = (M^T M + lambda I)^-1 M^T S per head, through the Schur
+ * complement of M^T M's diagonal x diagonal block (which is diagonal). With A =
+ * diag(n-|o|+lambda) over the 2n-1 diagonals and W = M^T M's diagonal x [columns, frame]
+ * block, S = C - W^T A^-1 W is (n+1) x (n+1):
+ *   moddit_fit_schur_host  writes S in closed form (fp64, row-major) into a HOST buffer
+ *                          of (n+1)^2 doubles; the caller inverts it once per
+ *                          (n, blocks_per_frame, lambda) and keeps the inverse on the device;
+ *   moddit_fit_lines       with schur_inv = S^-1 (device, fp64 (n+1)^2), mts (H,3n) fp32
+ *                          from moddit_mts, writes x (H,3n) fp32 in M's column order. Three
+ *                          kernels, fp64 arithmetic in a fixed order, x rounded once;
+ *                          workspace: moddit_fit_workspace_doubles(H, n) doubles (scratch).
+ * n <= 4096.
+ * Replaces the cached Cholesky factor and _solve_all_heads (MoD/mod/cuda_lstsq.py:141-208:
+ * torch.linalg.cholesky of the whole 3n x 3n M^T M, then cholesky_solve per call).
  */
-int moddit_solve(const float* ginv, const float* mts, float* x, int heads, int features,
-                 moddit_stream_t stream);
+int moddit_fit_schur_host(int n, int blocks_per_frame, double regularization, double* schur_out);
+int64_t moddit_fit_workspace_doubles(int heads, int n);
+int moddit_fit_lines(const double* schur_inv, const float* mts, float* x, double* workspace,
+                     int heads, int n, int blocks_per_frame, double regularization,
+                     moddit_stream_t stream);
 
 /*
  * Line prediction and selection: with c = X[:,2n-1:3n-1]/2 and d = X[:,:2n-1] for the

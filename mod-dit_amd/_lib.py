@@ -48,7 +48,9 @@ _SIGNATURES = {
                                  _f, _f, _i, _i, _i, _i, _i, _vp]),
     "moddit_mts": (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),
     "moddit_mtm_host": (_i, [_i, _i, ctypes.c_double, _vp]),
-    "moddit_solve": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "moddit_fit_schur_host": (_i, [_i, _i, ctypes.c_double, _vp]),
+    "moddit_fit_workspace_doubles": (ctypes.c_int64, [_i, _i]),
+    "moddit_fit_lines": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, ctypes.c_double, _vp]),
     "moddit_select_lines": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp]),
     "moddit_check_bd": (_i, [_vp, _i, _i, _f, _vp, _vp]),
     "moddit_mask_from_lines": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _i, _i, _i, _i,

@@ -446,9 +446,12 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
     for (int t = 0; t < 3; ++t)
       if (t < n_vt) dma_k(p.map_kt0 + t, t);
-    // tile 0 has landed once at most the two later tiles' DMAs are outstanding
+    // Each wave issues kWinPerWave DMAs per K tile (4 at d=128, 2 at d=64), and vector
+    // memory operations retire in issue order: tile 0 has landed once at most the two
+    // later tiles' DMAs are outstanding.
+    static_assert(3 * kWinPerWave < 16, "vmcnt immediate holds at most 15");
     if (n_vt >= 3)
-      MODDIT_WAIT_VM_LGKM0(8);
+      MODDIT_WAIT_VM_LGKM0(2 * kWinPerWave);
     else
       MODDIT_WAIT_VM_LGKM0(0);
     __syncthreads();
@@ -478,9 +481,9 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
       // tile j+1 must have landed; the DMAs of tiles j+2 and j+3 (and any map stores,
       // which are younger than tile j+1's DMA) may stay outstanding
       if (j + 3 < n_vt)
-        MODDIT_WAIT_VM_LGKM0(8);
+        MODDIT_WAIT_VM_LGKM0(2 * kWinPerWave);
       else if (j + 2 < n_vt)
-        MODDIT_WAIT_VM_LGKM0(4);
+        MODDIT_WAIT_VM_LGKM0(kWinPerWave);
       else
         MODDIT_WAIT_VM_LGKM0(0);
       __syncthreads();
@@ -524,14 +527,10 @@ int launch_attention_impl(const AttnParams& p, int batch, hipStream_t stream) {
   using L = AttnLds<D>;
   auto kernel = attention_fwd_kernel<D, E, kSparse, kRagged, kMap>;
   constexpr int kLds = L::kTotal + (kMap ? kMapCountBytes : 0);
-  static bool configured = false;  // the attribute is per function, same on every device
-  if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kLds) != hipSuccess) {
-      set_error("attention: cannot reserve %d bytes of LDS", kLds);
-      return MODDIT_EHIP;
-    }
-    configured = true;
+  static LaunchSetup once;
+  if (set_dynamic_lds_once(once, reinterpret_cast<const void*>(kernel), kLds) != hipSuccess) {
+    set_error("attention: cannot reserve %d bytes of LDS", kLds);
+    return MODDIT_EHIP;
   }
   const int64_t tiles = static_cast<int64_t>(batch) * p.heads * p.n_qtiles;
   if (tiles == 0) return MODDIT_OK;

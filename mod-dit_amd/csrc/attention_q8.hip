@@ -469,14 +469,10 @@ template <int D, typename E, bool kSparse, bool kRagged>
 int launch_q8_impl(const Q8Params& p, int batch, hipStream_t stream) {
   using L = Q8Lds<D>;
   auto kernel = attention_q8_kernel<D, E, kSparse, kRagged>;
-  static bool configured = false;
-  if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, L::kTotal) != hipSuccess) {
-      set_error("attention_q8: cannot reserve %d bytes of LDS", L::kTotal);
-      return MODDIT_EHIP;
-    }
-    configured = true;
+  static LaunchSetup once;
+  if (set_dynamic_lds_once(once, reinterpret_cast<const void*>(kernel), L::kTotal) != hipSuccess) {
+    set_error("attention_q8: cannot reserve %d bytes of LDS", L::kTotal);
+    return MODDIT_EHIP;
   }
   const int64_t tiles = static_cast<int64_t>(batch) * p.heads * p.n_qtiles;
   if (tiles == 0) return MODDIT_OK;

@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/moddit.h"
@@ -37,6 +38,31 @@ void clear_error();
   } while (0)
 
 inline hipStream_t as_stream(moddit_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------------------------
+// One-time launch setup. A kernel's dynamic-LDS limit (hipFuncSetAttribute) is set on
+// the current device, so it is set once per device. Concurrent first launches from
+// several host threads wait for the one that performs it (std::call_once), and every
+// caller sees its status. Declare one `static LaunchSetup` per kernel.
+// ---------------------------------------------------------------------------------
+constexpr int kMaxDevices = 64;
+
+struct LaunchSetup {
+  std::once_flag flag[kMaxDevices];
+  hipError_t status[kMaxDevices] = {};
+};
+
+inline hipError_t set_dynamic_lds_once(LaunchSetup& once, const void* kernel, int bytes) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  auto setup = [&] {
+    return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  };
+  if (dev < 0 || dev >= kMaxDevices) return setup();  // outside the table: every call
+  std::call_once(once.flag[dev], [&] { once.status[dev] = setup(); });
+  return once.status[dev];
+}
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

@@ -1,7 +1,7 @@
-// Mask prediction for gfx950: M^T S line statistics, the ridge solve, line
-// prediction/selection, block-diagonal mode, block mask + attention tile lists, and the
-// refresh merge. All of it is HBM-bound integer/byte work plus one skinny GEMM; none of
-// it is reshaped onto MFMA.
+// Mask prediction for gfx950: M^T S line statistics, line prediction/selection,
+// block-diagonal mode, block mask + attention tile lists, and the refresh merge (the
+// ridge solve between M^T S and the selection is in fit.hip). All of it is HBM-bound
+// integer/byte work; none of it is reshaped onto MFMA.
 //
 // Floating-point contraction is disabled in this file: the prediction
 // cur + (cur - last) / T must round exactly like the reference's separate fp32 ops.
@@ -178,65 +178,6 @@ __global__ __launch_bounds__(kMtsThreads) void mts_kernel(MtsParams p) {
   if (tid == 0) {
     Acc tot{s_fixed[0], s_wide[0], s_special[0]};
     p.out[static_cast<int64_t>(h) * F + F - 1] = acc_result(tot, p.fp16);
-  }
-}
-
-// =====================================================================================
-// X = Ginv . MTS^T (MoD/mod/cuda_lstsq.py:189-208)
-// =====================================================================================
-//
-// A skinny GEMM (F x F) . (F x H) bound by reading Ginv once. Workgroup = 16 rows of
-// Ginv x up to 32 heads; 16 threads per row stride the reduction dimension, MTS chunks
-// are staged in LDS and shared by the 16 rows. The order of summation is fixed, so the
-// result is deterministic.
-
-constexpr int kSolveThreads = 256;
-constexpr int kSolveRows = 16;
-constexpr int kSolveHeads = 32;
-constexpr int kSolveChunk = 256;
-
-__global__ __launch_bounds__(kSolveThreads) void solve_kernel(const float* __restrict__ ginv,
-                                                              const float* __restrict__ mts,
-                                                              float* __restrict__ x, int heads,
-                                                              int F) {
-  __shared__ float s_rhs[kSolveHeads][kSolveChunk];
-  const int tid = threadIdx.x;
-  const int r = tid / 16;
-  const int j = tid % 16;
-  const int row = blockIdx.x * kSolveRows + r;
-  const int h0 = blockIdx.y * kSolveHeads;
-  const int nh = heads - h0 < kSolveHeads ? heads - h0 : kSolveHeads;
-
-  float acc[kSolveHeads];
-#pragma unroll
-  for (int hh = 0; hh < kSolveHeads; ++hh) acc[hh] = 0.f;
-
-  const float* grow = ginv + static_cast<int64_t>(row < F ? row : F - 1) * F;
-  for (int k0 = 0; k0 < F; k0 += kSolveChunk) {
-    const int g = k0 + tid;
-    for (int hh = 0; hh < kSolveHeads; ++hh)
-      s_rhs[hh][tid] = (hh < nh && g < F) ? mts[static_cast<int64_t>(h0 + hh) * F + g] : 0.f;
-    __syncthreads();
-#pragma unroll 4
-    for (int m = 0; m < kSolveChunk / 16; ++m) {
-      const int gg = k0 + j + 16 * m;
-      const float a = gg < F ? grow[gg] : 0.f;
-#pragma unroll
-      for (int hh = 0; hh < kSolveHeads; ++hh) acc[hh] = __builtin_fmaf(a, s_rhs[hh][j + 16 * m], acc[hh]);
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int hh = 0; hh < kSolveHeads; ++hh) {
-    float v = acc[hh];
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    v += __shfl_xor(v, 8);
-    acc[hh] = v;
-  }
-  if (j == 0 && row < F) {
-    for (int hh = 0; hh < nh; ++hh) x[static_cast<int64_t>(h0 + hh) * F + row] = acc[hh];
   }
 }
 
@@ -648,19 +589,6 @@ extern "C" int moddit_mtm_host(int n, int blocks_per_frame, double regularizatio
   return MODDIT_OK;
 }
 
-extern "C" int moddit_solve(const float* ginv, const float* mts, float* x, int heads,
-                            int features, moddit_stream_t stream) {
-  clear_error();
-  MODDIT_CHECK_ARG(ginv && mts && x, "solve: null pointer argument");
-  MODDIT_CHECK_ARG(heads >= 0 && features > 0, "solve: invalid shape");
-  if (heads == 0) return MODDIT_OK;
-  dim3 grid((features + kSolveRows - 1) / kSolveRows, (heads + kSolveHeads - 1) / kSolveHeads);
-  hipLaunchKernelGGL(solve_kernel, grid, dim3(kSolveThreads), 0, as_stream(stream), ginv, mts, x,
-                     heads, features);
-  MODDIT_CHECK_LAUNCH("solve");
-  return MODDIT_OK;
-}
-
 extern "C" int moddit_select_lines(const float* x_cur, const float* x_last, int heads, int n,
                                    int predict_T, int top_k, int32_t* sel_out,
                                    moddit_stream_t stream) {
@@ -674,15 +602,11 @@ extern "C" int moddit_select_lines(const float* x_cur, const float* x_last, int 
   const int k = top_k < items ? top_k : items;
   if (heads == 0) return MODDIT_OK;
   const size_t lds = static_cast<size_t>(items) * sizeof(unsigned long long);
-  static bool configured = false;
-  if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(select_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            kSelMaxItems * 8) != hipSuccess) {
-      set_error("select_lines: cannot reserve LDS");
-      return MODDIT_EHIP;
-    }
-    configured = true;
+  static LaunchSetup once;
+  if (set_dynamic_lds_once(once, reinterpret_cast<const void*>(select_kernel),
+                           kSelMaxItems * 8) != hipSuccess) {
+    set_error("select_lines: cannot reserve LDS");
+    return MODDIT_EHIP;
   }
   hipLaunchKernelGGL(select_kernel, dim3(heads), dim3(kSelThreads), lds, as_stream(stream), x_cur,
                      x_last, n, 0.f, predict_T, k, sel_out);

@@ -224,14 +224,10 @@ template <int D, typename E, bool kRagged>
 int launch_replay_impl(const ReplayParams& p, int batch, hipStream_t stream) {
   using L = ReplayLds<D>;
   auto kernel = replay_map_kernel<D, E, kRagged>;
-  static bool configured = false;
-  if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, L::kTotal) != hipSuccess) {
-      set_error("sparsity_map: cannot reserve %d bytes of LDS", L::kTotal);
-      return MODDIT_EHIP;
-    }
-    configured = true;
+  static LaunchSetup once;
+  if (set_dynamic_lds_once(once, reinterpret_cast<const void*>(kernel), L::kTotal) != hipSuccess) {
+    set_error("sparsity_map: cannot reserve %d bytes of LDS", L::kTotal);
+    return MODDIT_EHIP;
   }
   const int64_t tiles = static_cast<int64_t>(batch) * p.heads * p.n_qtiles;
   if (tiles == 0) return MODDIT_OK;

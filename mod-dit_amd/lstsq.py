@@ -2,9 +2,13 @@
 
 min_X ||S - M X||^2 + lambda ||X||^2 with M's columns = [2n-1 block diagonals, n block
 columns, 1 frame-block-diagonal] over an (n, n) block map. M^T M depends only on
-(n, blocks_per_frame, lambda): it is built in closed form once, inverted once in fp64
-on the device (Cholesky, falling back to LU then pinv like :176-183) and cached as an
-fp32 matrix. Every fit is then one M^T S reduction kernel plus one skinny GEMM kernel.
+(n, blocks_per_frame, lambda), and its diagonal x diagonal block is diagonal, so the
+system reduces to the (n+1) x (n+1) Schur complement of that block. The complement is
+built in closed form once, inverted once in fp64 on the device (Cholesky, falling back
+to LU then pinv like :176-183) and cached in fp64. Every fit is then one M^T S
+reduction kernel plus the three fp64 kernels of `ops.fit_lines`; the features agree
+with the fp64 ridge solution to fp32 rounding (the reference's fp32 Cholesky of the
+full 3n x 3n matrix does not).
 """
 from __future__ import annotations
 
@@ -33,9 +37,10 @@ def _factor_cache_key(device: torch.device, n: int, blocks_per_frame: int, regul
     return (device.type, device.index, int(n), int(blocks_per_frame), float(regularization))
 
 
-def get_inverse(device: torch.device, n: int, blocks_per_frame: int,
-                regularization: float) -> torch.Tensor:
-    """Cached fp32 (M^T M + lambda I)^-1 on `device` (MoD/mod/cuda_lstsq.py:141-186)."""
+def get_factor(device: torch.device, n: int, blocks_per_frame: int,
+               regularization: float) -> torch.Tensor:
+    """Cached fp64 inverse of the (n+1, n+1) Schur complement on `device`
+    (the factor cache of MoD/mod/cuda_lstsq.py:141-186)."""
     key = _factor_cache_key(device, n, blocks_per_frame, regularization)
     inv = _FACTOR_CACHE.get(key)
     if inv is not None:
@@ -44,18 +49,23 @@ def get_inverse(device: torch.device, n: int, blocks_per_frame: int,
         inv = _FACTOR_CACHE.get(key)
         if inv is not None:
             return inv
-        mtm = compute_mtm(n, blocks_per_frame, regularization).to(device)
+        schur = ops.fit_schur_host(n, blocks_per_frame, regularization).to(device)
         try:
-            chol = torch.linalg.cholesky(mtm)
-            inv64 = torch.cholesky_inverse(chol)
+            inv = torch.cholesky_inverse(torch.linalg.cholesky(schur))
         except RuntimeError:
             try:
-                inv64 = torch.linalg.inv(mtm)
+                inv = torch.linalg.inv(schur)
             except RuntimeError:
-                inv64 = torch.linalg.pinv(mtm)
-        inv = inv64.to(torch.float32).contiguous()
+                inv = torch.linalg.pinv(schur)
+        inv = inv.contiguous()
         _FACTOR_CACHE[key] = inv
         return inv
+
+
+def fit(mts: torch.Tensor, n: int, blocks_per_frame: int, regularization: float) -> torch.Tensor:
+    """Features X (H, 3n) fp32 of M^T S rows (H, 3n)."""
+    sinv = get_factor(mts.device, n, blocks_per_frame, regularization)
+    return ops.fit_lines(sinv, mts, n, blocks_per_frame, regularization)
 
 
 def features_from_x(X: torch.Tensor, n: int) -> Dict[str, torch.Tensor]:
@@ -80,9 +90,7 @@ def solve_lstsq(warmup_state, S_T, step, blocks_per_frame, layer_idx=0, regulari
         raise ValueError("solve_lstsq: S_T must be a GPU tensor (this build has no CPU path)")
     H, n = S_T.shape[0], S_T.shape[1]
     if step > warmup_state["warmup_steps"] - 2:
-        mts = ops.compute_mts(S_T, blocks_per_frame)
-        ginv = get_inverse(S_T.device, n, blocks_per_frame, regularization)
-        X = ops.solve(ginv, mts)
+        X = fit(ops.compute_mts(S_T, blocks_per_frame), n, blocks_per_frame, regularization)
     else:
         X = torch.zeros((H, 3 * n), device=S_T.device, dtype=torch.float32)
     return features_from_x(X, n)

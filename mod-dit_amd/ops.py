@@ -329,16 +329,31 @@ def compute_mtm_host(n: int, blocks_per_frame: int, regularization: float) -> to
     return out
 
 
-def solve(ginv: torch.Tensor, mts: torch.Tensor) -> torch.Tensor:
-    """X = Ginv . MTS^T per head: (H, F) fp32."""
-    _require_gpu(ginv, mts, what="solve")
+def fit_schur_host(n: int, blocks_per_frame: int, regularization: float) -> torch.Tensor:
+    """Closed-form (n+1, n+1) Schur complement of M^T M + lambda I, CPU float64."""
+    out = torch.empty((n + 1, n + 1), dtype=torch.float64)
+    check(_lib.load().moddit_fit_schur_host(int(n), int(blocks_per_frame), float(regularization),
+                                            out.data_ptr()), "moddit_fit_schur_host")
+    return out
+
+
+def fit_lines(schur_inv: torch.Tensor, mts: torch.Tensor, n: int, blocks_per_frame: int,
+              regularization: float) -> torch.Tensor:
+    """Ridge fit X (H, 3n) fp32 of M^T S rows `mts` (H, 3n), given S^-1 (n+1, n+1) fp64."""
+    _require_gpu(schur_inv, mts, what="fit_lines")
     H, F = mts.shape
-    if ginv.shape != (F, F) or ginv.dtype != torch.float32 or mts.dtype != torch.float32:
-        raise ValueError("solve expects ginv (F,F) fp32 and mts (H,F) fp32")
-    ginv, mts = ginv.contiguous(), mts.contiguous()
+    if F != 3 * n or mts.dtype != torch.float32:
+        raise ValueError(f"fit_lines: mts must be (H, {3 * n}) fp32, got {tuple(mts.shape)} {mts.dtype}")
+    if schur_inv.shape != (n + 1, n + 1) or schur_inv.dtype != torch.float64:
+        raise ValueError(f"fit_lines: schur_inv must be ({n + 1}, {n + 1}) fp64")
+    schur_inv, mts = schur_inv.contiguous(), mts.contiguous()
+    lib = _lib.load()
+    ws = torch.empty(max(lib.moddit_fit_workspace_doubles(H, n), 1), device=mts.device,
+                     dtype=torch.float64)
     x = torch.empty_like(mts)
-    check(_lib.load().moddit_solve(ginv.data_ptr(), mts.data_ptr(), x.data_ptr(), H, F,
-                                   _stream(mts)), "moddit_solve")
+    check(lib.moddit_fit_lines(schur_inv.data_ptr(), mts.data_ptr(), x.data_ptr(), ws.data_ptr(),
+                               H, int(n), int(blocks_per_frame), float(regularization),
+                               _stream(mts)), "moddit_fit_lines")
     return x
 
 

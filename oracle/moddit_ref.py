@@ -13,9 +13,11 @@ import numpy as np
 __all__ = [
     "bf16_round", "fp16_round", "build_M", "mtm_closed_form", "mts_loop", "mts_exact",
     "ridge_solve", "features_from_x", "reconstruct_map", "predict_lines",
-    "choose_topk_lines", "generate_mask_from_lines", "mask_cell", "tiles_from_mask",
-    "token_mask_from_tiles", "token_mask_from_blocks", "masked_attention",
-    "probability_map", "replay_map", "refresh_merge", "step_phase", "video_layout",
+    "choose_topk_lines", "generate_mask_from_lines", "video_mask_cells", "mask_cell",
+    "tiles_from_mask",
+    "token_mask_from_tiles", "token_mask_rows_from_tiles", "token_mask_from_blocks",
+    "masked_attention",
+    "probability_map", "replay_map", "replay_map_rows", "refresh_merge", "step_phase", "video_layout",
     "cogvideox_grid", "e4m3_decode", "e4m3_encode", "quantize_qkv", "attention_q8",
     "MODE_SPARSE", "MODE_BLOCK_DIAGONAL", "MODE_FULL",
 ]
@@ -193,8 +195,7 @@ def _mts_f64(S2: np.ndarray, bpf: int) -> np.ndarray:
     r = np.arange(n)[:, None]
     c = np.arange(n)[None, :]
     dk = ((c - r) + (n - 1)).ravel()
-    d = np.zeros(nd)
-    np.add.at(d, dk, S2.ravel())
+    d = np.bincount(dk, weights=S2.ravel(), minlength=nd)
     cs = S2.sum(axis=0)
     nbk = n // bpf
     b = sum(S2[f * bpf:(f + 1) * bpf, f * bpf:(f + 1) * bpf].sum() for f in range(nbk))
@@ -318,6 +319,34 @@ def generate_mask_from_lines(sel: np.ndarray, modes: Sequence[int], *, seq_len: 
     return mask
 
 
+def video_mask_cells(sel: np.ndarray, modes: Sequence[int], n: int, bpf: int) -> np.ndarray:
+    """The per-cell definition of `mask_cell` evaluated for whole (H, n, n) video masks:
+    cell (i, j) is set iff the head is 'full', column j is selected, diagonal j - i is
+    selected, or the head is block-diagonal and i, j share a frame. For shapes where the
+    line-by-line restatement is slow (n = 1800)."""
+    sel = np.asarray(sel, dtype=np.int64)
+    H = len(modes)
+    out = np.zeros((H, n, n), dtype=bool)
+    r = np.arange(n)[:, None]
+    c = np.arange(n)[None, :]
+    diag_idx = (c - r) + (n - 1)
+    same_frame = (r // bpf) == (c // bpf)
+    for h in range(H):
+        if modes[h] == MODE_FULL:
+            out[h] = True
+            continue
+        col = np.zeros(n, dtype=bool)
+        dia = np.zeros(2 * n - 1, dtype=bool)
+        idx = sel[h]
+        col[idx[(idx >= 0) & (idx < n)]] = True
+        dd = idx[(idx >= n) & (idx < 3 * n - 1)] - n
+        dia[dd] = True
+        out[h] = col[None, :] | dia[diag_idx]
+        if modes[h] == MODE_BLOCK_DIAGONAL:
+            out[h] |= same_frame
+    return out
+
+
 def mask_cell(sel_h: Sequence[int], mode: int, n: int, bpf: int, i: int, j: int) -> bool:
     """Independent per-cell definition of the video mask (used to cross-check)."""
     if mode == MODE_FULL:
@@ -350,22 +379,19 @@ def tiles_from_mask(mask: np.ndarray, block_size: int, union_rows: bool,
     for h in range(H):
         hl = []
         for t in range(nq):
-            ent = []
             if block_size == 64:
                 r0, r1 = 2 * t, 2 * t + 1
-                for j in range(cols):
-                    m0 = bool(mask[h, r0, j]) if r0 < rows else False
-                    m1 = bool(mask[h, r1, j]) if r1 < rows else False
-                    if m0 or m1:
-                        bits = 3 if union_rows else (int(m0) | (int(m1) << 1))
-                        if j < kv_tiles:
-                            ent.append((j << 2) | bits)
+                m0 = mask[h, r0].astype(bool) if r0 < rows else np.zeros(cols, bool)
+                m1 = mask[h, r1].astype(bool) if r1 < rows else np.zeros(cols, bool)
+                js = np.nonzero((m0 | m1)[:kv_tiles])[0]
+                bits = (np.full(js.size, 3) if union_rows
+                        else m0[js].astype(np.int64) | (m1[js].astype(np.int64) << 1))
+                ent = ((js << 2) | bits).tolist()
             else:
-                for j in range(cols):
-                    if mask[h, t, j]:
-                        for s in range(2):
-                            if 2 * j + s < kv_tiles:
-                                ent.append(((2 * j + s) << 2) | 3)
+                js = np.nonzero(mask[h, t].astype(bool))[0]
+                kts = np.stack([2 * js, 2 * js + 1], axis=1).reshape(-1)  # ascending
+                kts = kts[kts < kv_tiles]
+                ent = ((kts << 2) | 3).tolist()
             counts[h, t] = len(ent)
             hl.append(ent)
         lists.append(hl)
@@ -393,6 +419,25 @@ def token_mask_from_tiles(lists, H: int, q_len: int, kv_len: int, origin: int = 
     return m
 
 
+def token_mask_rows_from_tiles(counts_h: np.ndarray, entries_h: np.ndarray, rows: np.ndarray,
+                               kv_len: int, origin: int = 0) -> np.ndarray:
+    """Rows `rows` (token indices) of one head's token-level mask, (len(rows), kv_len),
+    from tile arrays as the kernel reads them: counts (n_qtiles,), entries
+    (n_qtiles, cap) with entry = key_tile << 2 | row bits on the grid starting at token
+    `origin`. Equals token_mask_from_tiles(...)[h, rows] without forming all rows."""
+    rows = np.asarray(rows, dtype=np.int64)
+    out = np.zeros((rows.size, kv_len), dtype=bool)
+    for i, r in enumerate(rows):
+        g = r - origin  # grid row
+        t, half = g // 128, (g % 128) // 64
+        ent = np.asarray(entries_h[t, :counts_h[t]], dtype=np.int64)
+        for kt in (ent[(ent >> half) & 1 == 1] >> 2):
+            k0, k1 = max(kt * 64 + origin, 0), min(kt * 64 + 64 + origin, kv_len)
+            if k0 < k1:
+                out[i, k0:k1] = True
+    return out
+
+
 def token_mask_from_blocks(mask: np.ndarray, block_size: int) -> np.ndarray:
     """Expand an (H, nb, nb) block mask to tokens."""
     return np.repeat(np.repeat(mask, block_size, axis=1), block_size, axis=2)
@@ -414,7 +459,7 @@ def masked_attention(q, k, v, token_mask: Optional[np.ndarray] = None, scale=Non
     D = q.shape[-1]
     if scale is None:
         scale = D ** -0.5
-    s = np.einsum("hqd,hkd->hqk", q, k).astype(dtype) * dtype(scale)
+    s = np.matmul(q, np.swapaxes(k, -1, -2)).astype(dtype) * dtype(scale)
     if token_mask is not None:
         s = np.where(token_mask, s, -np.inf)
     m = s.max(axis=-1, keepdims=True)
@@ -422,7 +467,7 @@ def masked_attention(q, k, v, token_mask: Optional[np.ndarray] = None, scale=Non
     m = np.where(empty, 0, m)
     p = np.exp(s - m)
     l = p.sum(axis=-1, keepdims=True)
-    out = np.einsum("hqk,hkd->hqd", p, v) / np.where(l > 0, l, 1)
+    out = np.matmul(p, v) / np.where(l > 0, l, 1)
     out = np.where(l > 0, out, 0)
     with np.errstate(divide="ignore"):
         lse = np.where(l[..., 0] > 0, np.log(np.where(l[..., 0] > 0, l[..., 0], 1)) + m[..., 0], -np.inf)
@@ -477,6 +522,30 @@ def replay_map(q, k, lse, *, scale: float, log_threshold: float, q_off: int, k_o
         below[:nq, :nk] = (qs[h] @ kk[h].T) < thr[h][:, None].astype(np.float64)
         cnt = below.reshape(video_blocks, block_size, video_blocks, block_size).sum(axis=(1, 3))
         out[h] = (cnt.astype(np.float32) / np.float32(block_size * block_size)).astype(np.float16)
+    return out
+
+
+def replay_map_rows(q, k, lse, blocks, *, scale: float, log_threshold: float,
+                    video_blocks: int, block_size: int, dtype: str = "bf16") -> np.ndarray:
+    """Rows `blocks` (query block indices) of replay_map for a video-only layout
+    (offsets 0, whole blocks): (H, len(blocks), video_blocks) fp16. Same arithmetic as
+    replay_map, for shapes whose full map is too large to form on the host."""
+    rnd = bf16_round if dtype == "bf16" else fp16_round
+    q = np.asarray(q, dtype=np.float32)
+    k = np.asarray(k, dtype=np.float32)
+    H = q.shape[0]
+    bs = block_size
+    vt = video_blocks * bs
+    kk = k[:, :vt].astype(np.float64)
+    out = np.zeros((H, len(blocks), video_blocks), dtype=np.float16)
+    for h in range(H):
+        for i, b in enumerate(blocks):
+            r0, r1 = b * bs, b * bs + bs
+            qs = rnd(q[h, r0:r1] * np.float32(scale)).astype(np.float64)
+            thr = (np.asarray(lse, np.float32)[h, r0:r1] + np.float32(log_threshold)).astype(np.float32)
+            below = (qs @ kk[h].T) < thr[:, None].astype(np.float64)
+            cnt = below.reshape(bs, video_blocks, bs).sum(axis=(0, 2))
+            out[h, i] = (cnt.astype(np.float32) / np.float32(bs * bs)).astype(np.float16)
     return out
 
 

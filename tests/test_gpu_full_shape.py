@@ -1,0 +1,256 @@
+"""Full-shape parity of the MOD-DiT step machine on the benchmark's Wan-like and
+HunyuanVideo-like (headline) layers, plus the end-to-end mask agreement (GPU only).
+
+SparseAttentionWithMap (MoD/mod/attn_mask.py:567-729) runs the reference schedule
+(W=12, T=10) at the real shape on seeded structured inputs that change from step to
+step. Each stage is checked against the oracle given the GPU's own input to that stage:
+  - map steps: the map on sampled query blocks against the replay oracle with the
+    kernel's LSE (the reference's count bound, tests/test_flash_sparsity.py:100-101);
+    the output (the dense pass) on sampled rows against fp64 attention;
+  - the fit of every head against the fp64 ridge solution of the full 3n x 3n system
+    (MoD/mod/cuda_lstsq.py:189-264), to fp32 rounding;
+  - modes, selected lines, the mask and the tile lists bit-exactly on a head subset;
+  - the refresh merge bit-exactly (attn_mask.py:663-675);
+  - sparse steps: sampled rows of the first and last head (whole first and last query
+    tiles, and one row in every query tile, so every workgroup-order deal round is hit)
+    against fp64 attention under the executed mask, and every output row written (the
+    sparse kernel on the state's tiles into a NaN-filled output equals the step
+    machine's output).
+Tolerance of attention outputs: the north-star bound, max-abs <= 2e-2 and mean-abs <=
+2e-3, with half a bf16 ulp of |ref| admitted on sparse rows (counted and printed).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+import mod_dit_amd as md
+import oracle as O
+from mod_dit_amd import ops
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+DEV = "cuda"
+W, T, THR, BS = 12, 10, 1e-4, 64
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _check(err, ref, tag, sparse):
+    slack = err > 2e-2
+    _say(f"{tag}: max-abs {err.max():.3e} mean-abs {err.mean():.3e} "
+         f"beyond 2e-2: {int(slack.sum())} of {err.size}")
+    bound = 2e-2 + (2.0 ** -9) * np.abs(ref) if sparse else 2e-2
+    assert np.all(err <= bound) and err.mean() <= 2e-3, (tag, err.max(), err.mean())
+    assert slack.sum() <= 1e-3 * err.size and np.all(np.abs(ref[slack]) >= 1.0), tag
+
+
+def _sample_rows(N):
+    t = np.arange(N // 128)
+    return np.unique(np.r_[0:128, N - 128:N, t * 128 + (t * 53) % 128])
+
+
+def _check_rows(out, q, k, v, h, rows, allowed, tag, sparse):
+    """fp64 attention of head h at `rows` (chunks of 256) under `allowed(rows) -> mask`."""
+    qh = _np(q[0, h]).astype(np.float64)
+    kh = _np(k[0, h]).astype(np.float64)
+    vh = _np(v[0, h]).astype(np.float64)
+    oh = _np(out[0, h])
+    errs, refs = [], []
+    for c in range(0, rows.size, 256):
+        r = rows[c:c + 256]
+        tm = None if allowed is None else allowed(r)[None]
+        ref, _ = O.masked_attention(qh[None, r], kh[None], vh[None], tm, dtype=np.float64)
+        errs.append(np.abs(oh[r].astype(np.float64) - ref[0]))
+        refs.append(ref[0])
+    _check(np.concatenate(errs), np.concatenate(refs), tag, sparse)
+
+
+def _inputs(base, step):
+    """The step's q/k/v: the seeded structured layer plus N(0, 0.25^2) noise per step."""
+    g = torch.Generator(device=DEV).manual_seed(1000 + step)
+    return tuple((t.float() + 0.25 * torch.randn(t.shape, generator=g, device=DEV)).to(t.dtype)
+                 for t in base)
+
+
+def _check_map(smap, q, k, v, heads, blocks, n, D):
+    """Rows `blocks` of an (H, n, n) map against the replay oracle with the kernel's LSE
+    (the map step runs this same dense kernel; it is deterministic)."""
+    _, lse = ops.flash_fwd(q, k, v, return_lse=True)
+    for h in heads:
+        ref = O.replay_map_rows(_np(q[0, h:h + 1]), _np(k[0, h:h + 1]), _np(lse[0, h:h + 1]),
+                                blocks, scale=D ** -0.5, log_threshold=math.log(THR),
+                                video_blocks=n, block_size=BS)[0]
+        got = smap[h, blocks].cpu().numpy()
+        err = np.abs(got.astype(np.float32) - ref.astype(np.float32)) * BS * BS
+        _say(f"map head {h}: max count difference {err.max():.1f} over {err.size} cells, "
+             f"{len(np.unique(ref))} distinct values")
+        assert err.max() <= 2.1
+
+
+def _check_fit(st, bpf):
+    X = st["features_history"][-1]["_x"].cpu().numpy().astype(np.float64)
+    Xr = O.ridge_solve(st["prev_full_maps"].cpu().numpy().astype(np.float64), bpf, 1.0)
+    rel = np.abs(X - Xr).max() / np.abs(Xr).max()
+    _say(f"fit: max err / max|X| = {rel:.3e} over {X.shape[0]} heads")
+    assert rel <= 2e-6
+    return Xr
+
+
+def _check_lines_mask_tiles(st, heads, n, bpf, N, top_k, Xr=None):
+    """Modes, lines, mask and tiles of `heads` bit-exact given the GPU features; with the
+    oracle's fp64 fit Xr, also the agreement of the lines it would select."""
+    hist = st["features_history"]
+    xc = hist[-1]["_x"].cpu().numpy()
+    xl = hist[-2]["_x"].cpu().numpy()
+    modes_all = [O.MODE_BLOCK_DIAGONAL if m == "block_diagonal" else O.MODE_SPARSE
+                 for m in st["mode"]]
+    sel = O.choose_topk_lines(xc[heads], xl[heads], n, T, top_k)
+    modes = [modes_all[h] for h in heads]
+    mask_ref = O.video_mask_cells(sel, modes, n, bpf)  # wan layout: the video mask
+    mask = st["mask"][heads].cpu().numpy()
+    assert np.array_equal(mask, mask_ref)
+    counts, lists = O.tiles_from_mask(mask_ref, BS, union_rows=False)
+    tiles = st["_tiles"]
+    assert st["_tiles_for"] is st["mask"]
+    got_c = tiles.counts[heads].cpu().numpy()
+    got_e = tiles.entries[heads].cpu().numpy()
+    assert np.array_equal(got_c, counts)
+    for i in range(len(heads)):
+        for t in range(counts.shape[1]):
+            assert got_e[i, t, :counts[i, t]].tolist() == lists[i][t]
+    sp = 1.0 - st["mask"].float().mean().item()
+    _say(f"mask sparsity {sp:.4f} (top_k {top_k}); lines/mask/tiles bit-exact on heads {heads}")
+    if Xr is not None:
+        x64 = Xr.astype(np.float32)
+        sel64 = O.choose_topk_lines(x64, xl, n, T, top_k)
+        sel_gpu = O.choose_topk_lines(xc, xl, n, T, top_k)
+        agree = np.mean([len(set(a) & set(b)) / len(a) for a, b in zip(sel64, sel_gpu)])
+        _say(f"lines selected from the oracle's fp64 fit of the GPU map: agreement {agree:.5f}")
+        assert agree >= 0.999
+    return sp
+
+
+def _check_sparse_step(st, out, q, k, v, heads, N):
+    tiles = st["_tiles"]
+    assert st["_tiles_for"] is st["mask"]
+    o_nan = torch.full_like(q, float("nan"))
+    ops.block_sparse_fwd(q, k, v, tiles, out=o_nan)
+    assert not torch.isnan(o_nan).any(), "rows left unwritten"
+    assert torch.equal(o_nan, out)
+    counts = tiles.counts.cpu().numpy()
+    entries = tiles.entries.cpu().numpy()
+    rows = _sample_rows(N)
+    for h in heads:
+        allowed = lambda r, h=h: O.token_mask_rows_from_tiles(counts[h], entries[h], r, N)
+        _check_rows(out, q, k, v, h, rows, allowed, f"sparse head {h}", sparse=True)
+
+
+def _run_layer(name, steps, top_k_at):
+    c = bench.CONFIGS[name]
+    H, F, Hp, Wp, D = c["H"], c["F"], c["Hp"], c["Wp"], c["D"]
+    N = F * Hp * Wp
+    n, bpf = N // BS, (Hp * Wp) // BS
+    _say(f"[{name}] H={H} N={N} d={D} n={n}: synthesising inputs")
+    base = bench.synth_qkv(H, F, Hp, Wp, D, seed=0)
+    st = md.create_adaptive_mask_state("wan", H, N, 0, Hp * Wp, F, warmup_steps=W,
+                                       top_k=top_k_at[min(top_k_at)], predict_T=T, threshold=THR,
+                                       block_size=BS, tile_rows="exact")
+    heads = [0, H - 1]
+    rows = _sample_rows(N)
+    for step in steps:
+        st["top_k"] = top_k_at.get(step, st["top_k"])
+        phase = O.step_phase(step, W, T)
+        _say(f"[{name}] step {step} ({phase}), top_k {st['top_k']}")
+        q, k, v = _inputs(base, step)
+        prev_mask = st.get("mask")
+        prev_maps = st.get("prev_full_maps")
+        out, info = md.SparseAttentionWithMap(q, k, v, st, None, current_step=step)
+        torch.cuda.synchronize()
+        assert out.shape == q.shape
+        if phase == "sparse":
+            _check_sparse_step(st, out, q, k, v, heads, N)
+            continue
+        for h in heads:  # map steps return the dense pass
+            _check_rows(out, q, k, v, h, rows, None, f"dense head {h}", sparse=False)
+        blocks = [0, 1, n // 2, n - 1]
+        if phase == "refresh":
+            cur = md.flash_attn_with_sparsity_map(q, k, v, THR, BS, model_type="wan")[1][0]
+            _check_map(cur, q, k, v, heads, blocks, n, D)
+            merged = O.refresh_merge(prev_maps.cpu().numpy(), cur.cpu().numpy(),
+                                     prev_mask.cpu().numpy())
+            assert np.array_equal(st["prev_full_maps"].cpu().numpy(), merged)
+            del cur, merged
+        else:
+            _check_map(st["prev_full_maps"], q, k, v, heads, blocks, n, D)
+        if phase == "map_fit":
+            assert torch.count_nonzero(st["features_history"][-1]["_x"]).item() == 0
+            continue
+        Xr = _check_fit(st, bpf)
+        if phase == "map_fit_predict":
+            xc = st["features_history"][-1]["_x"].cpu().numpy()
+            want = ["block_diagonal" if x <= 1.0 else "sparse" for x in xc[:, -1]]
+            assert list(st["mode"]) == want
+        sp = _check_lines_mask_tiles(st, heads, n, bpf, N, st["top_k"], Xr)
+        assert 0.6 < sp < 0.95
+        del q, k, v, out
+    return st
+
+
+def test_headline_layer_trajectory_stage_by_stage():
+    """HunyuanVideo-like headline layer (H=24, N=115,200, d=128, n=1800): the last two
+    warmup steps (map + fit, then predict), the first sparse step, the refresh at step
+    21 and the sparse step after it, with top_k ramping from 461 (~83 % sparsity) to 400
+    at the refresh (the sweep's rising sparsity)."""
+    _run_layer("hunyuan", [W - 2, W - 1, W, W + T - 1, W + T], {W - 2: 461, W + T - 1: 400})
+
+
+def test_wan_layer_stage_by_stage():
+    """Wan2.1-14B-like layer (H=40, N=69,120, d=128, n=1080): map + fit, predict, first
+    sparse step, at top_k 273 (~81 % sparsity)."""
+    _run_layer("wan", [W - 2, W - 1, W], {W - 2: 273})
+
+
+def test_end_to_end_mask_agreement_plumbing_config():
+    """configs[0] shape (B=1, H=2, N=4096 = 4 frames x 32x32, d=64; Q/K/V ~ N(0,1) from a
+    seed, bf16 on the GPU): the mask predicted by the GPU path from raw inputs (map steps
+    W-2 and W-1) against the oracle's prediction from the same inputs (fp64 LSE, replay,
+    fp64 ridge fit, selection, mask). Reports the agreement of modes, lines and mask
+    cells; the oracle's own arithmetic differs from the GPU's only in rounding."""
+    H, F, tpf, D = 2, 4, 1024, 64
+    N, n, bpf = F * tpf, F * tpf // BS, tpf // BS
+    rng = np.random.default_rng(0)
+    qn, kn, vn = (O.bf16_round(rng.normal(size=(H, N, D)).astype(np.float32)) for _ in range(3))
+    q, k, v = (torch.from_numpy(t[None]).to(torch.bfloat16).to(DEV) for t in (qn, kn, vn))
+    _, lse = O.masked_attention(qn, kn, vn, None, dtype=np.float64)
+    smap = O.replay_map(qn, kn, lse.astype(np.float32), scale=D ** -0.5,
+                        log_threshold=math.log(THR), q_off=0, k_off=0, video_blocks=n,
+                        block_size=BS)
+    X = O.ridge_solve(smap.astype(np.float64), bpf, 1.0).astype(np.float32)
+    modes = [O.MODE_BLOCK_DIAGONAL if x <= 1.0 else O.MODE_SPARSE for x in X[:, -1]]
+    for top_k in (16, 48):
+        st = md.create_adaptive_mask_state("wan", H, N, 0, tpf, F, warmup_steps=W, top_k=top_k,
+                                           predict_T=T, threshold=THR, block_size=BS,
+                                           tile_rows="exact")
+        for step in (W - 2, W - 1):
+            md.SparseAttentionWithMap(q, k, v, st, None, current_step=step)
+        sel = O.choose_topk_lines(X, np.zeros_like(X), n, T, top_k)
+        mask = O.generate_mask_from_lines(sel, modes, seq_len=N, block_size=BS, video_tokens=N,
+                                          text_tokens=0, bpf=bpf, model_type="wan")
+        xg = st["features_history"][-1]["_x"].cpu().numpy()
+        sel_g = O.choose_topk_lines(xg, np.zeros_like(xg), n, T, top_k)
+        mode_agree = list(st["mode"]) == ["block_diagonal" if m else "sparse" for m in modes]
+        line_agree = np.mean([len(set(a) & set(b)) / top_k for a, b in zip(sel, sel_g)])
+        cell_agree = float((st["mask"].cpu().numpy() == mask).mean())
+        map_cells = float((st["prev_full_maps"].cpu().numpy() == smap[:, :, :]).mean())
+        _say(f"top_k {top_k}: map cells equal {map_cells:.5f}, modes equal {mode_agree}, "
+             f"line agreement {line_agree:.5f}, mask-cell agreement {cell_agree:.5f}, "
+             f"sparsity {1 - mask.mean():.4f}")
+        assert mode_agree and line_agree >= 0.98 and cell_agree >= 0.99

@@ -92,11 +92,13 @@ def test_mask_to_tiles_bit_exact(nb, bs, union):
     assert lists == rlists
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("union", [False, True])
-def test_block_sparse_config1_matches_masked_fp64(union):
-    # small plumbing shape: B=1, H=2, N=4096, d=64, 64x64 blocks, 50% random mask, diagonal on
+def test_block_sparse_config1_matches_masked_fp64(union, dtype):
+    # small plumbing shape: B=1, H=2, N=4096, d=64, 64x64 blocks, 50% random mask, diagonal
+    # on; fp16 is the dtype the reference runs CogVideoX in (inference/cogvideo_test.py:48)
     H, S, D, bs = 2, 4096, 64, 64
-    q, k, v = (_randn((1, H, S, D), 200 + i, torch.bfloat16) for i in range(3))
+    q, k, v = (_randn((1, H, S, D), 200 + i, dtype) for i in range(3))
     m = _random_block_mask(H, S // bs, 0.5, 5)
     tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=union)
     out, lse = ops.block_sparse_fwd(q, k, v, tiles, return_lse=True)
@@ -105,7 +107,7 @@ def test_block_sparse_config1_matches_masked_fp64(union):
     if not union:
         assert np.array_equal(tm, O.token_mask_from_blocks(m, bs))
     ref, ref_lse = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), tm, dtype=np.float64)
-    _check_attn(out[0], ref, f"sparse config1 union={union}")
+    _check_attn(out[0], ref, f"sparse config1 union={union} {dtype}")
     np.testing.assert_allclose(_np(lse[0]), ref_lse, rtol=0, atol=2e-3)
 
 
@@ -126,26 +128,30 @@ def test_block_sparse_all_true_equals_dense_and_empty_rows_are_zero():
     assert torch.all(torch.isneginf(lse[:, :, 192:256]))
 
 
-def test_block_sparse_bs128_mask():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_block_sparse_bs128_mask(dtype):
     H, S, D, bs = 2, 1024, 128, 128
-    q, k, v = (_randn((1, H, S, D), 400 + i, torch.bfloat16) for i in range(3))
+    q, k, v = (_randn((1, H, S, D), 400 + i, dtype) for i in range(3))
     m = _random_block_mask(H, S // bs, 0.3, 11)
     tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs)
     out, _ = ops.block_sparse_fwd(q, k, v, tiles)
     ref, _ = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), O.token_mask_from_blocks(m, bs),
                                 dtype=np.float64)
-    _check_attn(out[0], ref, "sparse bs128")
+    _check_attn(out[0], ref, f"sparse bs128 {dtype}")
 
 
-@pytest.mark.parametrize("text,video,D,union", [(50, 450, 64, False), (50, 450, 128, True),
-                                                (226, 1350, 64, False), (100, 200, 128, False)])
-def test_block_sparse_shifted_grid_matches_masked_fp64(text, video, D, union):
+@pytest.mark.parametrize("text,video,D,union,dtype", [
+    (50, 450, 64, False, torch.bfloat16), (50, 450, 128, True, torch.bfloat16),
+    (226, 1350, 64, False, torch.bfloat16), (100, 200, 128, False, torch.bfloat16),
+    (226, 1350, 64, False, torch.float16), (50, 450, 128, True, torch.float16),
+])
+def test_block_sparse_shifted_grid_matches_masked_fp64(text, video, D, union, dtype):
     # text-first sequence with text not block-aligned: the tile grid starts
     # origin = text - 64*ceil(text/64) tokens before token 0 (this build's padding rule)
     H, bs = 2, 64
     S = text + video
     tb, vb, origin = O.cogvideox_grid(text, video, bs)
-    q, k, v = (_randn((1, H, S, D), 600 + i, torch.bfloat16) for i in range(3))
+    q, k, v = (_randn((1, H, S, D), 600 + i, dtype) for i in range(3))
     m = _random_block_mask(H, tb + vb, 0.35, 21)
     m[:, 1, :] = False  # a grid row whose queries attend to nothing
     tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=union, grid_origin=origin)
@@ -154,7 +160,7 @@ def test_block_sparse_shifted_grid_matches_masked_fp64(text, video, D, union):
     _, lists = _tiles_np(tiles)
     tm = O.token_mask_from_tiles(lists, H, S, S, origin=origin)
     ref, ref_lse = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), tm, dtype=np.float64)
-    _check_attn(out[0], ref, f"shifted grid text={text} video={video} D={D} union={union}")
+    _check_attn(out[0], ref, f"shifted grid text={text} video={video} D={D} union={union} {dtype}")
     np.testing.assert_allclose(_np(lse[0]), ref_lse, rtol=0, atol=2e-3)
 
 
@@ -296,23 +302,28 @@ def test_sparsity_map_partial_last_block_dyadic_bit_exact(text, video, bs, D, dt
 ])
 def test_flash_fwd_map_fused_pass(model_type, video, text, bs, D, dtype):
     """Dense pass + map in one kernel: the map is bit-exact to the replay of the kernel's
-    own LSE (oracle and the separate replay kernel), O/LSE match the dense kernel."""
+    own LSE (oracle and the separate replay kernel), O/LSE match the dense kernel.
+
+    Q and K are multiples of 1/4 in [-2, 2], so every score is exact in fp32 and the
+    probabilities span the threshold: the map holds dozens of distinct counts per head,
+    and a key tile read from the wrong ring stage changes them."""
     S = video + text
     rng = np.random.default_rng(S + bs + D)
-    qn = rng.integers(-4, 5, size=(1, 2, S, D)).astype(np.float32) / 8
-    kn = rng.integers(-4, 5, size=(1, 2, S, D)).astype(np.float32) / 8
+    qn = rng.integers(-8, 9, size=(1, 2, S, D)).astype(np.float32) / 4
+    kn = rng.integers(-8, 9, size=(1, 2, S, D)).astype(np.float32) / 4
     q = torch.from_numpy(qn).to(dtype).to(DEV)
     k = torch.from_numpy(kn).to(dtype).to(DEV)
     v = _randn((1, 2, S, D), 900, dtype)
     scale = D ** -0.5
     vb, qo, _ = O.video_layout(model_type, S, video, text, bs)
-    ln_thr = math.log(1e-2)
+    ln_thr = math.log(1e-3)
     out, lse, smap = ops.flash_fwd_map(q, k, v, softmax_scale=scale, log_threshold=ln_thr,
                                        video_offset=qo, video_blocks=vb, block_size=bs)
     assert smap.shape == (1, 2, vb, vb) and smap.dtype == torch.float16
     dt = "bf16" if dtype == torch.bfloat16 else "fp16"
     ref = O.replay_map(qn[0], kn[0], _np(lse[0]), scale=scale, log_threshold=ln_thr, q_off=qo,
                        k_off=qo, video_blocks=vb, block_size=bs, dtype=dt)
+    assert len(np.unique(ref)) >= 16  # an informative map, not a constant one
     assert np.array_equal(smap[0].cpu().numpy(), ref)
     sep = md.cuda_sparsity_map(q, k, lse, softmax_scale=scale, log_threshold=ln_thr,
                                q_video_offset=qo, k_video_offset=qo, video_blocks=vb, block_size=bs)
@@ -321,7 +332,7 @@ def test_flash_fwd_map_fused_pass(model_type, video, text, bs, D, dtype):
     # (FMA contraction may differ, so P can round differently): close to it, and
     # deterministic across calls
     o2, lse2 = ops.flash_fwd(q, k, v)
-    assert (out.float() - o2.float()).abs().max().item() <= 4e-3
+    assert ((out.float() - o2.float()).abs() <= 4e-3 + o2.float().abs() * 2.0 ** -7).all()
     if qo % 128 == 0:
         assert (lse - lse2).abs().max().item() <= 1e-5
     out3, lse3, smap3 = ops.flash_fwd_map(q, k, v, softmax_scale=scale, log_threshold=ln_thr,
@@ -424,8 +435,12 @@ def test_mts_arbitrary_fp16_and_fp32_inputs():
     np.testing.assert_allclose(got32, want, rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize("n,bpf", [(64, 16), (270, 21)])
+@pytest.mark.parametrize("n,bpf", [(64, 16), (270, 21), (1080, 60), (1800, 60)])
 def test_solve_lstsq_matches_fp64_ridge(n, bpf):
+    """The fit (M^T S kernel + the three fp64 Schur-complement kernels) against the fp64
+    ridge solution of the full 3n x 3n system, up to the Wan-like (n=1080) and headline
+    (n=1800) shapes: agreement to fp32 rounding of X, and the same selected lines as
+    the oracle's selection on the fp64 fit."""
     rng = np.random.default_rng(n)
     H = 3
     S = (rng.integers(0, 4097, size=(H, n, n)) / 4096.0).astype(np.float16)
@@ -435,10 +450,18 @@ def test_solve_lstsq_matches_fp64_ridge(n, bpf):
     X = O.ridge_solve(S.astype(np.float64), bpf, 1.0)
     got = feats["_x"].cpu().numpy().astype(np.float64)
     scale = np.abs(X).max()
-    print(f"solve n={n}: max rel err {np.abs(got - X).max() / scale:.3e}", flush=True)
-    assert np.abs(got - X).max() <= 1e-4 * scale
+    err = np.abs(got - X).max() / scale
+    print(f"fit n={n}: max err / max|X| = {err:.3e}", flush=True)
+    assert err <= 2e-6
     f = O.features_from_x(got.astype(np.float32), n)
     assert np.array_equal(feats["c"].cpu().numpy(), f["c"])
+    zero_hist = np.zeros_like(X, dtype=np.float32)
+    k = n // 3
+    sel_gpu = O.choose_topk_lines(got.astype(np.float32), zero_hist, n, 10, k)
+    sel_f64 = O.choose_topk_lines(X.astype(np.float32), zero_hist, n, 10, k)
+    agree = np.mean([len(set(a) & set(b)) / k for a, b in zip(sel_gpu, sel_f64)])
+    print(f"fit n={n}: selected-line agreement with the fp64 fit {agree:.5f}", flush=True)
+    assert agree >= 0.999
     zero = md.solve_lstsq(st, torch.from_numpy(S).to(DEV), step=st["warmup_steps"] - 2, blocks_per_frame=bpf)
     assert torch.count_nonzero(zero["_x"]).item() == 0
 

@@ -43,9 +43,20 @@ def _np(t):
 
 
 def _check(out, ref, tag, sparse=False):
+    """North-star bound (max-abs 2e-2, mean-abs 2e-3). Sparse rows attend to few keys, so
+    outputs can reach |o| ~ 4, where the bf16 output quantum alone is 2^-7: there the
+    elementwise bound also admits half a bf16 ulp of |ref| (2^-9 |ref|). How many
+    elements use that slack is printed, and they must be rare (<= 0.1 %) and large
+    (|ref| >= 1, where half an ulp is >= 2^-9)."""
     err = np.abs(_np(out).astype(np.float64) - ref)
     bound = 2e-2 + (2.0 ** -9) * np.abs(ref) if sparse else 2e-2
+    slack = err > 2e-2
+    n_slack = int(slack.sum())
+    print(f"{tag}: max-abs {err.max():.3e} mean-abs {err.mean():.3e} "
+          f"beyond 2e-2: {n_slack} of {err.size}", flush=True)
     assert np.all(err <= bound) and err.mean() <= 2e-3, (tag, err.max(), err.mean())
+    assert n_slack <= 1e-3 * err.size, (tag, n_slack)
+    assert np.all(np.abs(ref[slack]) >= 1.0), (tag, "slack used at |ref| < 1")
 
 
 class MockAttention(torch.nn.Module):
@@ -440,8 +451,11 @@ def test_processors_with_int8_precision(layout):
     assert n_sparse >= 2
 
 
-@pytest.mark.parametrize("tile_rows", ["exact", "union"])
-def test_cogvideox_processor_per_sample_states_and_shifted_grid(tile_rows):
+@pytest.mark.parametrize("tile_rows,dtype", [("exact", torch.bfloat16), ("union", torch.bfloat16),
+                                             ("exact", torch.float16)])
+def test_cogvideox_processor_per_sample_states_and_shifted_grid(tile_rows, dtype):
+    """CogVideoX call site; fp16 is the dtype the reference runs it in
+    (MoD/inference/cogvideo_test.py:48)."""
     H, D, F, tpf, bs, B = 2, 64, 3, 150, 64, 2
     text, video = 50, F * tpf  # neither block-aligned: the grid starts 14 tokens early
     S, C = text + video, H * D
@@ -450,7 +464,7 @@ def test_cogvideox_processor_per_sample_states_and_shifted_grid(tile_rows):
                                             top_k=top_k, predict_T=T, threshold=thr,
                                             block_size=bs, tile_rows=tile_rows)
               for _ in range(B)]
-    attn = MockAttention(C, H, seed=5, norm_dim=D).to(DEV).to(torch.bfloat16)
+    attn = MockAttention(C, H, seed=5, norm_dim=D).to(DEV).to(dtype)
     rec = Recorder()
     procs = [CogVideoXProcessor(states, layer_idx=li, dense_block=1, dense_timestep=0,
                                 attention_fn=rec) for li in range(2)]
@@ -459,8 +473,8 @@ def test_cogvideox_processor_per_sample_states_and_shifted_grid(tile_rows):
     pos = torch.randn(video, C, generator=g)
     with torch.no_grad():
         for i in range(steps):
-            x = (torch.randn(B, video, C, generator=g) * 0.5 + pos).to(torch.bfloat16).to(DEV)
-            e = torch.randn(B, text, C, generator=g).to(torch.bfloat16).to(DEV)
+            x = (torch.randn(B, video, C, generator=g) * 0.5 + pos).to(dtype).to(DEV)
+            e = torch.randn(B, text, C, generator=g).to(dtype).to(DEV)
             for p in procs:
                 out, enc = p(attn, x, e, rot, timestep=torch.tensor([999 - i]),
                              numeral_timestep=i)

@@ -37,11 +37,19 @@ def _np(t):
 
 def _check_attn(out, ref, tag, sparse=False):
     """North-star bound (max-abs 2e-2, mean-abs 2e-3). Sparse rows attend to few keys, so
-    outputs can reach |o| ~ 4 where the bf16 output quantum alone is 2^-7; there the
-    elementwise bound also admits half a bf16 ulp of |ref| (2^-9 |ref|)."""
+    outputs can reach |o| ~ 4, where the bf16 output quantum alone is 2^-7: there the
+    elementwise bound also admits half a bf16 ulp of |ref| (2^-9 |ref|). How many
+    elements use that slack is printed, and they must be rare (<= 0.1 %) and large
+    (|ref| >= 1, where half an ulp is >= 2^-9)."""
     err = np.abs(_np(out).astype(np.float64) - ref)
     bound = 2e-2 + (2.0 ** -9) * np.abs(ref) if sparse else 2e-2
+    slack = err > 2e-2
+    n_slack = int(slack.sum())
+    print(f"{tag}: max-abs {err.max():.3e} mean-abs {err.mean():.3e} "
+          f"beyond 2e-2: {n_slack} of {err.size}", flush=True)
     assert np.all(err <= bound) and err.mean() <= 2e-3, (tag, err.max(), err.mean())
+    assert n_slack <= 1e-3 * err.size, (tag, n_slack)
+    assert np.all(np.abs(ref[slack]) >= 1.0), (tag, "slack used at |ref| < 1")
 
 
 def _structured_qkv(H, F, tpf, D, seed):
@@ -93,7 +101,7 @@ def test_schedule_matches_oracle_stage_by_stage(tile_rows):
                 assert np.all(X == 0)  # zero features at W-2
             else:
                 Xr = O.ridge_solve(S_fit.astype(np.float64), bpf, 1.0)
-                assert np.abs(X - Xr).max() <= 1e-4 * max(np.abs(Xr).max(), 1e-6)
+                assert np.abs(X - Xr).max() <= 2e-6 * max(np.abs(Xr).max(), 1e-6)
             if phase == "refresh":
                 # prev = where(mask, current map, prev) over the video blocks
                 smap = md.flash_attn_with_sparsity_map(q, k, v, thr, bs, model_type="wan")[1][0]

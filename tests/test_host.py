@@ -38,6 +38,33 @@ def test_mtm_host_matches_oracle_closed_form_and_brute_force():
     assert np.array_equal(md.compute_mtm(9, 4, 0.5).numpy(), M.T @ M + 0.5 * np.eye(27))
 
 
+def test_fit_schur_host_is_the_schur_complement_of_mtm():
+    """S = C - W^T A^-1 W for G = M^T M + lambda I = [[A, W], [W^T, C]] with A the
+    diagonal x diagonal block, which must be diagonal; the fit's elimination rests on it.
+    Checked against the explicit indicator matrix M (brute force) and the closed form."""
+    for n, bpf, lam in [(4, 2, 1.0), (9, 4, 0.5), (37, 5, 1.0), (64, 16, 1.0), (61, 60, 1.0)]:
+        G = O.build_M(n, bpf) if n <= 16 else None
+        G = G.T @ G + lam * np.eye(3 * n) if G is not None else O.mtm_closed_form(n, bpf, lam)
+        nd = 2 * n - 1
+        A = G[:nd, :nd]
+        assert np.array_equal(A, np.diag(np.diag(A)))
+        W, C = G[:nd, nd:], G[nd:, nd:]
+        want = C - W.T @ (W / np.diag(A)[:, None])
+        got = md.ops.fit_schur_host(n, bpf, lam).numpy()
+        np.testing.assert_allclose(got, want, rtol=0, atol=1e-12 * np.abs(want).max())
+        # eliminating A and solving S reproduces the full solve
+        rng = np.random.default_rng(n)
+        rhs = rng.normal(size=3 * n)
+        x_full = np.linalg.solve(G, rhs)
+        x_cb = np.linalg.solve(got, rhs[nd:] - W.T @ (rhs[:nd] / np.diag(A)))
+        x_d = (rhs[:nd] - W @ x_cb) / np.diag(A)
+        np.testing.assert_allclose(np.concatenate([x_d, x_cb]), x_full, rtol=0,
+                                   atol=1e-9 * np.abs(x_full).max())
+    lib = _lib.load()
+    assert lib.moddit_fit_schur_host(0, 1, 1.0, None) == _lib.MODDIT_EINVAL
+    assert lib.moddit_fit_workspace_doubles(24, 1800) == 2 * 24 * 1801
+
+
 def test_c_abi_rejects_bad_arguments_before_any_launch():
     lib = _lib.load()
     rc = lib.moddit_mtm_host(0, 1, 1.0, None)

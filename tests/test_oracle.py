@@ -208,6 +208,44 @@ def test_tiles_realise_the_mask(nb, bs):
             assert keys == sorted(keys) and len(keys) == counts[h, t]
 
 
+def _as_arrays(counts, lists):
+    H, nq = counts.shape
+    cap = max(1, max((len(e) for hl in lists for e in hl), default=1))
+    ent = np.zeros((H, nq, cap), np.int64)
+    for h in range(H):
+        for t in range(nq):
+            ent[h, t, :counts[h, t]] = lists[h][t]
+    return ent
+
+
+@pytest.mark.parametrize("nb,bs,union,kv_tiles,text,video", [
+    (9, 64, False, None, 0, 0), (9, 64, True, 13, 0, 0), (4, 128, False, 7, 0, 0),
+    (8, 64, False, None, 50, 450),
+])
+def test_token_mask_rows_equal_the_full_token_mask(nb, bs, union, kv_tiles, text, video):
+    """Row sampling of the executed mask (used at full shape, where the whole token mask
+    cannot be formed) equals the rows of the full token mask, incl. dropped key tiles
+    beyond kv_tiles and a shifted grid."""
+    rng = np.random.default_rng(nb + bs)
+    origin = 0
+    if text:
+        tb, vb, origin = O.cogvideox_grid(text, video, bs)
+        nb = tb + vb
+        S = text + video
+    else:
+        S = nb * bs
+    mask = rng.random((2, nb, nb)) < 0.35
+    counts, lists = O.tiles_from_mask(mask, bs, union_rows=union, kv_tiles=kv_tiles)
+    ent = _as_arrays(counts, lists)
+    full = O.token_mask_from_tiles(lists, 2, S, S, origin=origin)
+    rows = np.unique(np.r_[0, S - 1, rng.integers(0, S, 40)])
+    for h in range(2):
+        got = O.token_mask_rows_from_tiles(counts[h], ent[h], rows, S, origin=origin)
+        assert np.array_equal(got, full[h, rows])
+    if kv_tiles is not None:  # nothing at or beyond the key-tile limit
+        assert not full[:, :, kv_tiles * 64 + origin:].any()
+
+
 @pytest.mark.parametrize("text,video,bs", [(50, 450, 64), (226, 1350, 64), (100, 700, 128),
                                            (128, 512, 64)])
 def test_cogvideox_grid_puts_text_and_video_on_block_boundaries(text, video, bs):
@@ -457,3 +495,32 @@ def test_attention_q8_lazy_max_and_masks():
                                    rtol=0, atol=1e-9)
     # the bound is not loose by orders of magnitude: the rounding error does show
     assert np.abs(o - ref_o)[:, keep].max() > 0.05 * bound[:, keep].max()
+
+
+@pytest.mark.parametrize("bs,D", [(64, 64), (128, 128)])
+def test_replay_map_rows_equal_rows_of_the_full_replay(bs, D):
+    rng = np.random.default_rng(bs + D)
+    H, nb = 2, 4
+    S = nb * bs
+    q = O.bf16_round(rng.normal(size=(H, S, D)).astype(np.float32))
+    k = O.bf16_round(rng.normal(size=(H, S, D)).astype(np.float32))
+    _, lse = O.masked_attention(q, k, k, None, dtype=np.float64)
+    lse = lse.astype(np.float32)
+    kw = dict(scale=D ** -0.5, log_threshold=np.log(1e-3), video_blocks=nb, block_size=bs)
+    full = O.replay_map(q, k, lse, q_off=0, k_off=0, **kw)
+    blocks = [3, 0, 2]
+    assert np.array_equal(O.replay_map_rows(q, k, lse, blocks, **kw), full[:, blocks])
+
+
+@pytest.mark.parametrize("n,bpf,k", [(7, 3, 4), (30, 6, 20), (64, 16, 48)])
+def test_video_mask_cells_equal_the_line_by_line_restatement(n, bpf, k):
+    rng = np.random.default_rng(n + k)
+    modes = [O.MODE_SPARSE, O.MODE_BLOCK_DIAGONAL, O.MODE_FULL, O.MODE_SPARSE]
+    sel = np.stack([np.sort(rng.choice(3 * n - 1, size=k, replace=False)) for _ in modes])
+    want = O.generate_mask_from_lines(sel, modes, seq_len=n * 64, block_size=64,
+                                      video_tokens=n * 64, text_tokens=0, bpf=bpf,
+                                      model_type="wan")
+    assert np.array_equal(O.video_mask_cells(sel, modes, n, bpf), want)
+    for h in (0, 1):  # and the scalar cell definition on a sample of cells
+        for i, j in rng.integers(0, n, size=(50, 2)):
+            assert want[h, i, j] == O.mask_cell(sel[h], modes[h], n, bpf, i, j)
