@@ -226,6 +226,20 @@ int moddit_fit_lines(const double* schur_inv, const float* mts, float* x, double
                      moddit_stream_t stream);
 
 /*
+ * moddit_fit_lines without a workspace argument and without any allocation: the
+ * workspace lives in a fixed device array of the library (2 * 64 * 2049 doubles =
+ * 2.1 MB per device, held until the process ends), so heads * (n + 1) <= 64 * 2049
+ * (e.g. 64 heads at n <= 2048; the headline's 24 heads at n = 1800 fit); larger shapes
+ * return MODDIT_EINVAL. Same kernels and results as moddit_fit_lines. Calls that overlap
+ * on one device share the array and race; serialise them (one stream per device).
+ * No counterpart in the reference: this entry point is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops).
+ */
+int moddit_fit_lines_noalloc(const double* schur_inv, const float* mts, float* x, int heads,
+                             int n, int blocks_per_frame, double regularization,
+                             moddit_stream_t stream);
+
+/*
  * Line prediction and selection: with c = X[:,2n-1:3n-1]/2 and d = X[:,:2n-1] for the
  * current (x_cur) and previous (x_last) fits, pred = cur + (cur - last) / predict_T over
  * v = [pred_c (n), pred_d (2n-1)]; selects the k = min(top_k, 3n-1) smallest per head,

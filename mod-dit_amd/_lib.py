@@ -51,6 +51,7 @@ _SIGNATURES = {
     "moddit_fit_schur_host": (_i, [_i, _i, ctypes.c_double, _vp]),
     "moddit_fit_workspace_doubles": (ctypes.c_int64, [_i, _i]),
     "moddit_fit_lines": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, ctypes.c_double, _vp]),
+    "moddit_fit_lines_noalloc": (_i, [_vp, _vp, _vp, _i, _i, _i, ctypes.c_double, _vp]),
     "moddit_select_lines": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp]),
     "moddit_check_bd": (_i, [_vp, _i, _i, _f, _vp, _vp]),
     "moddit_mask_from_lines": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _i, _i, _i, _i,

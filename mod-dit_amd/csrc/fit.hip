@@ -211,6 +211,19 @@ __global__ __launch_bounds__(kFitThreads) void fit_diag_kernel(const float* __re
 
 constexpr int kFitMaxN = 4096;  // LDS: 4n-1 doubles per workgroup (128 KB at the limit)
 
+// Scratch of the allocation-free entry point moddit_fit_lines_noalloc: room for the
+// workspace of up to 64 heads at n <= 2048 (2 * 64 * 2049 doubles = 2.1 MB per device,
+// held until the process ends). Host code never uses this name as an address: it
+// resolves the device address once per device with hipGetSymbolAddress.
+constexpr int64_t kNoAllocDoubles = 2 * int64_t{64} * 2049;
+__device__ __align__(256) double scratch[kNoAllocDoubles];
+
+struct ScratchAddr {
+  std::once_flag flag[kMaxDevices];
+  hipError_t status[kMaxDevices] = {};
+  double* ptr[kMaxDevices] = {};
+};
+
 }  // namespace
 }  // namespace moddit
 
@@ -268,18 +281,21 @@ extern "C" int64_t moddit_fit_workspace_doubles(int heads, int n) {
   return 2 * static_cast<int64_t>(heads) * (static_cast<int64_t>(n) + 1);
 }
 
-extern "C" int moddit_fit_lines(const double* schur_inv, const float* mts, float* x,
-                                double* workspace, int heads, int n, int blocks_per_frame,
-                                double regularization, moddit_stream_t stream) {
-  using namespace moddit;
-  clear_error();
-  MODDIT_CHECK_ARG(schur_inv && mts && x && workspace, "fit_lines: null pointer argument");
+namespace moddit {
+namespace {
+
+int check_fit_args(const double* schur_inv, const float* mts, float* x, int heads, int n,
+                   int blocks_per_frame, double regularization) {
+  MODDIT_CHECK_ARG(schur_inv && mts && x, "fit_lines: null pointer argument");
   MODDIT_CHECK_ARG(heads >= 0 && n > 0 && blocks_per_frame > 0,
                    "fit_lines: invalid shape heads=%d n=%d bpf=%d", heads, n, blocks_per_frame);
   MODDIT_CHECK_ARG(n <= kFitMaxN, "fit_lines: n=%d exceeds %d", n, kFitMaxN);
   MODDIT_CHECK_ARG(regularization >= 0.0, "fit_lines: regularization must be >= 0");
-  if (heads == 0) return MODDIT_OK;
-  hipStream_t st = as_stream(stream);
+  return MODDIT_OK;
+}
+
+int launch_fit(const double* schur_inv, const float* mts, float* x, double* workspace, int heads,
+               int n, int blocks_per_frame, double regularization, hipStream_t st) {
   const int m = n + 1;
   double* y = workspace;
   double* xcb = workspace + static_cast<int64_t>(heads) * m;
@@ -303,4 +319,58 @@ extern "C" int moddit_fit_lines(const double* schur_inv, const float* mts, float
                      blocks_per_frame, regularization);
   MODDIT_CHECK_LAUNCH("fit_lines (diag)");
   return MODDIT_OK;
+}
+
+}  // namespace
+}  // namespace moddit
+
+extern "C" int moddit_fit_lines(const double* schur_inv, const float* mts, float* x,
+                                double* workspace, int heads, int n, int blocks_per_frame,
+                                double regularization, moddit_stream_t stream) {
+  using namespace moddit;
+  clear_error();
+  int rc = check_fit_args(schur_inv, mts, x, heads, n, blocks_per_frame, regularization);
+  if (rc) return rc;
+  MODDIT_CHECK_ARG(workspace != nullptr, "fit_lines: null workspace");
+  if (heads == 0) return MODDIT_OK;
+  return launch_fit(schur_inv, mts, x, workspace, heads, n, blocks_per_frame, regularization,
+                    as_stream(stream));
+}
+
+// The same fit with its workspace in the library's device array `scratch` instead of a
+// caller buffer: no allocation of any kind. The array's device address is looked up once
+// per device (with that device current) and kept; calls that overlap on one device share
+// the array and race. Nothing in it needs to start at zero: every call writes the whole
+// workspace it reads.
+extern "C" int moddit_fit_lines_noalloc(const double* schur_inv, const float* mts, float* x,
+                                        int heads, int n, int blocks_per_frame,
+                                        double regularization, moddit_stream_t stream) {
+  using namespace moddit;
+  clear_error();
+  int rc = check_fit_args(schur_inv, mts, x, heads, n, blocks_per_frame, regularization);
+  if (rc) return rc;
+  const int64_t need = moddit_fit_workspace_doubles(heads, n);
+  MODDIT_CHECK_ARG(need <= kNoAllocDoubles,
+                   "fit_lines_noalloc: %d heads at n=%d need %lld doubles of scratch, the "
+                   "fixed array holds %lld (e.g. 64 heads at n <= 2048)",
+                   heads, n, static_cast<long long>(need), static_cast<long long>(kNoAllocDoubles));
+  if (heads == 0) return MODDIT_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("fit_lines_noalloc: no usable current device");
+    return MODDIT_EHIP;
+  }
+  static ScratchAddr addr;
+  std::call_once(addr.flag[dev], [&] {
+    void* p = nullptr;
+    addr.status[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    addr.ptr[dev] = static_cast<double*>(p);
+  });
+  if (addr.status[dev] != hipSuccess || addr.ptr[dev] == nullptr) {
+    set_error("fit_lines_noalloc: hipGetSymbolAddress failed: %s",
+              hipGetErrorString(addr.status[dev]));
+    return MODDIT_EHIP;
+  }
+  return launch_fit(schur_inv, mts, x, addr.ptr[dev], heads, n, blocks_per_frame, regularization,
+                    as_stream(stream));
 }
