@@ -292,55 +292,92 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
 
 
 # ------------------------------------------------------------------------------------
-# CPU baseline (the oracle's block-sparse attention on a bounded sample)
+# CPU baseline: the reference's PyTorch path restated in torch on the host cores
 # ------------------------------------------------------------------------------------
-def cpu_baseline(q, k, v, tiles, budget_s=12.0, what="the headline layer with the predicted mask"):
-    import numpy as np
+def cpu_baseline(q, k, v, tiles, *, smap, x_cur, x_last, modes, n, bpf, T, top_k, threshold,
+                 video_only=True, attn_budget_s=8.0, what="the headline layer"):
+    """Times the reference's CPU algorithms (oracle/cpu_path.py, torch on the CPU with
+    torch.get_num_threads() threads) on this run's inputs, stage by stage:
+      M^T S as written (cuda_lstsq.py:91-139, Python loops) and vectorised; M^T M
+      (:42-89), its Cholesky factor (:176-183, once per shape) and cholesky_solve
+      (:202-207, per call); topk (attn_mask.py:363-369); the per-line mask loop
+      (:440-559); the chunked probability map (:151-222); block-sparse attention
+      (the engine's semantics, :296-317).
+    Stages too slow to run whole are timed on a bounded sample and scaled to the full
+    call (listed under "extrapolated"). `value` is block-sparse attention in effective
+    (dense-equivalent) TFLOP/s, the GPU line's metric."""
+    import oracle.cpu_path as C
 
-    import oracle as O
+    threads = torch.get_num_threads()
+    H, N, D = q.shape[1], q.shape[2], q.shape[3]
+    st = {}
+    extrap = {}
+    with torch.no_grad():
+        S_T = smap.float().cpu().contiguous()  # the reference fits the fp32 copy (:231)
+        # M^T S as written: the diagonal loops on the 16 longest diagonals, scaled by cells
+        sample = [kd for kd in range(n - 9, n + 7) if 0 <= kd < 2 * n - 1]
+        cells = sum(n - abs(kd - (n - 1)) for kd in sample)
+        t_diag = C.timed(lambda: C.compute_mts_as_written(S_T, bpf, diagonals=sample))
+        t_rest = C.timed(lambda: C.compute_mts_as_written(S_T, bpf, diagonals=[], rest=True))
+        st["mts_as_written_s"] = t_diag * n * n / cells + t_rest
+        extrap["mts_as_written_s"] = f"diagonal loops timed on {len(sample)} of {2 * n - 1} diagonals"
+        st["mts_vectorized_s"] = C.timed(lambda: C.compute_mts_vectorized(S_T, bpf))
+        mts = C.compute_mts_vectorized(S_T, bpf)
+        G = None
 
-    try:
-        from threadpoolctl import threadpool_info
+        def build():
+            nonlocal G
+            G = C.compute_mtm(n, bpf, 1.0)
+        st["mtm_build_s"] = C.timed(build)
+        L = None
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
-    h = 0
-    N, D = q.shape[2], q.shape[3]
-    qh = q[0, h].float().cpu().numpy()
-    kh = k[0, h].float().cpu().numpy()
-    vh = v[0, h].float().cpu().numpy()
-    counts = tiles.counts[h].cpu().numpy()
-    entries = tiles.entries[h].cpu().numpy()
-    t0 = time.perf_counter()
-    rows = 0
-    org = int(tiles.origin)  # grid row / column 0 is token org (<= 0)
-    for t in range(counts.shape[0]):
-        ent = entries[t, :counts[t]]
-        for half in range(2):
-            r0, r1 = max(org + t * 128 + 64 * half, 0), min(org + t * 128 + 64 * half + 64, N)
-            if r0 >= r1:
-                continue
-            kts = [int(e >> 2) for e in ent if e & (1 << half)]
-            if not kts:
-                continue
-            idx = np.concatenate([np.arange(max(org + kt * 64, 0), min(org + kt * 64 + 64, N))
-                                  for kt in kts])
-            O.masked_attention(qh[None, r0:r1], kh[None, idx], vh[None, idx], None,
-                               dtype=np.float32)
-            rows += r1 - r0
-        if time.perf_counter() - t0 > budget_s:
-            break
-    dt = time.perf_counter() - t0
-    eff_flop = 4.0 * rows * N * D
+        def chol():
+            nonlocal L
+            L = torch.linalg.cholesky(G)
+        st["cholesky_once_s"] = C.timed(chol)
+        st["cholesky_solve_s"] = C.timed(lambda: torch.cholesky_solve(mts.t().contiguous(), L))
+        xc, xl = x_cur.float().cpu(), x_last.float().cpu()
+        st["topk_s"] = C.timed(lambda: C.choose_topk(xc, xl, n, T, top_k))
+        sel = C.choose_topk(xc, xl, n, T, top_k)
+        bd = modes.cpu() == 1
+        n_lines = min(8, sel.shape[1])
+        t_mask = C.timed(lambda: C.mask_from_lines_loop(sel, bd, n, bpf, lines=n_lines))
+        st["mask_loop_s"] = t_mask * sel.shape[1] / n_lines
+        extrap["mask_loop_s"] = f"{n_lines} of {sel.shape[1]} line passes timed"
+        st["mask_step_s"] = (st["mts_vectorized_s"] + st["cholesky_solve_s"] + st["topk_s"]
+                             + st["mask_loop_s"])
+        qh, kh, vh = (t[0, 0].float().cpu().contiguous() for t in (q, k, v))
+        if video_only:
+            chunks = 2
+            t_map = C.timed(lambda: [C.probability_map_chunk(qh, kh, vh, 8 * c, 8 * c + 8, 64,
+                                                             threshold) for c in range(chunks)])
+            st["probability_map_s"] = t_map / chunks * (n / 8) * H
+            extrap["probability_map_s"] = f"{chunks} chunks of 8 query blocks of head 0"
+        counts = tiles.counts[0].cpu().tolist()
+        entries = tiles.entries[0].cpu()
+        t0 = time.perf_counter()
+        rows = 0
+        for t in range(len(counts)):
+            ent = entries[t, :counts[t]].tolist()
+            rows += C.block_sparse_attention_tile(qh, kh, vh, t, ent, int(tiles.origin)).shape[0]
+            if time.perf_counter() - t0 > attn_budget_s:
+                break
+        dt = time.perf_counter() - t0
+        st["block_sparse_attention_s"] = dt * (N * H) / max(rows, 1)
+        extrap["block_sparse_attention_s"] = f"head 0, first {rows} of {N} query rows"
     return {
-        "value": eff_flop / dt / 1e12,
+        "value": 4.0 * rows * N * D / dt / 1e12,
         "unit": "TFLOP/s",
-        "cores": int(threads),
+        "cores": threads,
         "kind": "port",
-        "sample": f"head 0, first {rows} query rows of {what} (numpy fp32 oracle, active key "
-                  f"blocks only); {dt:.1f} s; effective (dense-equivalent) FLOPs of the sample / "
-                  f"time",
+        "sample": f"torch-CPU restatement of the reference's PyTorch path on {what}: "
+                  f"block-sparse attention (fp32) on head 0, first {rows} query rows, "
+                  f"{dt:.1f} s; effective (dense-equivalent) FLOPs of the sample / time",
+        "cpu_model": C.cpu_model(),
+        "torch_threads": threads,
+        "os_cpu_count": os.cpu_count(),
+        "stages_s": {kk: round(vv, 4) for kk, vv in st.items()},
+        "extrapolated": extrap,
     }
 
 
@@ -435,7 +472,10 @@ def run_mask_config(name, *, steps, warmup, no_cpu):
     overhead()
     ov = time_events(overhead, 10)
     overhead_ms = sorted(ov)[len(ov) // 2]
-    cpu = None if no_cpu else cpu_baseline(q, k, v, tiles, what=f"the {name} layer")
+    cpu = None if no_cpu else cpu_baseline(
+        q, k, v, tiles, smap=smap, x_cur=x0, x_last=x_last, modes=modes, n=vb, bpf=bpf, T=10,
+        top_k=top_k, threshold=1e-4, video_only=not text, attn_budget_s=4.0,
+        what=f"the {name} layer")
     exec_flop = 4.0 * D * 64 * 64 * pairs
     return {
         "metric": f"block-sparse attn effective TFLOP/s + ms/call, {name} configuration",
@@ -650,7 +690,10 @@ def main(argv=None):
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
-        cpu = cpu_baseline(q, k, v, tiles)
+        cpu = cpu_baseline(q, k, v, tiles, smap=art["smap"], x_cur=art["x_cur"],
+                           x_last=art["x_last"], modes=art["modes"], n=art["n"], bpf=bpf,
+                           T=art["T"], top_k=art["top_k"], threshold=args.threshold,
+                           what=f"the {args.config}-like layer")
 
     achieved = exec_flop / (kernel_ms * 1e-3) / 1e12
     traffic, traffic_src = measured_traffic() if args.config == "hunyuan" else (None, None)
