@@ -189,12 +189,16 @@ int moddit_sparsity_map(const void* q, const void* k, const float* lse, void* ma
  *   [0, 2n-1)   diagonal sums, index k <-> offset k-(n-1) (col - row)
  *   [2n-1, 3n-1) column sums
  *   3n-1        sum over the n/bpf frame-diagonal bpf x bpf blocks
- * map: contiguous (H,n,n) of map_dtype (FP16: summed exactly in 2^-24 fixed point and
- * rounded once to fp32; FP32: summed in fp64 and rounded once).
+ * map: contiguous (H,n,n) of map_dtype.
+ *   FP16 (n <= 8192): one pass over the map, summed exactly in int64 units of 2^-24 and
+ *        rounded once to fp32 (deterministic); needs a workspace of
+ *        moddit_mts_workspace_bytes(heads, n) bytes, 16-byte aligned (scratch);
+ *   FP32: summed in fp64 and rounded once; workspace may be NULL.
  * Replaces compute_mts (MoD/mod/cuda_lstsq_kernel.cu:421-482, kernels :17-162).
  */
 int moddit_mts(const void* map, int map_dtype, int heads, int n, int blocks_per_frame,
-               float* mts_out, moddit_stream_t stream);
+               void* workspace, float* mts_out, moddit_stream_t stream);
+int64_t moddit_mts_workspace_bytes(int heads, int n);
 
 /*
  * Closed-form M^T M + lambda*I (F = 3n) written as doubles into a HOST buffer of F*F.

@@ -126,12 +126,14 @@ __global__ __launch_bounds__(kFitThreads) void fit_rhs_kernel(const float* __res
   if (threadIdx.x == 0) yh[n] = static_cast<double>(m[F - 1]) - wb;
 }
 
-// x_cb[h] = S^-1 y[h] for all heads. Workgroup = 8 rows of S^-1 x up to 16 heads; 32
-// threads per row stride the reduction, y chunks are staged in LDS and shared by the rows.
+// x_cb[h] = S^-1 y[h] for all heads. Workgroup = 16 rows of S^-1 x up to 16 heads; 16
+// threads per row stride the reduction, and y chunks are staged in LDS and shared by the
+// rows (measured at n = 1800, H = 24: the fastest of the row x head blockings tried).
 constexpr int kGemvThreads = 256;
-constexpr int kGemvRows = 8;
+constexpr int kGemvRows = 16;
+constexpr int kGemvLanes = kGemvThreads / kGemvRows;  // threads per row
 constexpr int kGemvHeads = 16;
-constexpr int kGemvChunk = 256;
+constexpr int kGemvChunk = 128;
 
 __global__ __launch_bounds__(kGemvThreads) void fit_gemv_kernel(const double* __restrict__ sinv,
                                                                 const double* __restrict__ y,
@@ -139,8 +141,8 @@ __global__ __launch_bounds__(kGemvThreads) void fit_gemv_kernel(const double* __
                                                                 int heads, int m) {
   __shared__ double s_y[kGemvHeads][kGemvChunk];
   const int tid = threadIdx.x;
-  const int r = tid / 32;
-  const int j = tid % 32;
+  const int r = tid / kGemvLanes;
+  const int j = tid % kGemvLanes;
   const int row = blockIdx.x * kGemvRows + r;
   const int h0 = blockIdx.y * kGemvHeads;
   const int nh = heads - h0 < kGemvHeads ? heads - h0 : kGemvHeads;
@@ -149,17 +151,18 @@ __global__ __launch_bounds__(kGemvThreads) void fit_gemv_kernel(const double* __
   for (int hh = 0; hh < kGemvHeads; ++hh) acc[hh] = 0.0;
   const double* srow = sinv + static_cast<int64_t>(row < m ? row : m - 1) * m;
   for (int k0 = 0; k0 < m; k0 += kGemvChunk) {
-    for (int hh = 0; hh < kGemvHeads; ++hh) {
-      const int g = k0 + tid;
-      s_y[hh][tid] = (hh < nh && g < m) ? y[static_cast<int64_t>(h0 + hh) * m + g] : 0.0;
+    for (int i = tid; i < kGemvHeads * kGemvChunk; i += kGemvThreads) {
+      const int hh = i / kGemvChunk;
+      const int g = k0 + i % kGemvChunk;
+      s_y[hh][i % kGemvChunk] = (hh < nh && g < m) ? y[static_cast<int64_t>(h0 + hh) * m + g] : 0.0;
     }
     __syncthreads();
-#pragma unroll 2
-    for (int t = 0; t < kGemvChunk / 32; ++t) {
-      const int g = k0 + j + 32 * t;
+#pragma unroll
+    for (int t = 0; t < kGemvChunk / kGemvLanes; ++t) {
+      const int g = k0 + j + kGemvLanes * t;
       const double a = g < m ? srow[g] : 0.0;
 #pragma unroll
-      for (int hh = 0; hh < kGemvHeads; ++hh) acc[hh] = __builtin_fma(a, s_y[hh][j + 32 * t], acc[hh]);
+      for (int hh = 0; hh < kGemvHeads; ++hh) acc[hh] = __builtin_fma(a, s_y[hh][j + kGemvLanes * t], acc[hh]);
     }
     __syncthreads();
   }
@@ -167,11 +170,14 @@ __global__ __launch_bounds__(kGemvThreads) void fit_gemv_kernel(const double* __
   for (int hh = 0; hh < kGemvHeads; ++hh) {
     double v = acc[hh];
 #pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    for (int o = kGemvLanes / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
     acc[hh] = v;
   }
-  if (j == 0 && row < m)
-    for (int hh = 0; hh < nh; ++hh) xcb[static_cast<int64_t>(h0 + hh) * m + row] = acc[hh];
+  if (j == 0 && row < m) {
+#pragma unroll
+    for (int hh = 0; hh < kGemvHeads; ++hh)
+      if (hh < nh) xcb[static_cast<int64_t>(h0 + hh) * m + row] = acc[hh];
+  }
 }
 
 // One workgroup per head: x_d = A^-1 (m_d - B x_c - db x_b), X = [x_d, x_c, x_b] in fp32.

@@ -16,21 +16,17 @@ namespace {
 // M^T S (MoD/mod/cuda_lstsq_kernel.cu:17-162, 421-482; torch twin cuda_lstsq.py:91-139)
 // =====================================================================================
 //
-// Three workgroup roles over one launch, all reading the map with 128-byte rows per
-// wave:
+// fp32 maps: three workgroup roles over one launch, all reading the map with 128-byte
+// rows per wave:
 //   diagonal bands  : 64 diagonals per workgroup, lane = diagonal, waves stride rows
 //   column strips   : 64 columns per workgroup, lane = column, waves stride rows
 //   frame blocks    : one workgroup per head sums the n/bpf diagonal bpf x bpf blocks
-// fp16 inputs accumulate exactly as int64 multiples of 2^-24 (every fp16 value is one),
-// so each output is the correctly rounded fp32 of the exact sum whatever the order;
-// infinities/NaN are carried separately with float semantics. fp32 inputs accumulate
-// in fp64.
+// Sums accumulate in fp64 and are rounded once (deterministic: fixed order).
 
 constexpr int kMtsThreads = 256;
 
 struct MtsParams {
-  const void* map;
-  int fp16;
+  const float* map;
   int heads;
   int n;
   int bpf;
@@ -39,47 +35,8 @@ struct MtsParams {
   float* out;    // (H, 3n)
 };
 
-struct Acc {
-  long long fixed;  // fp16 inputs: sum in units of 2^-24
-  double wide;      // fp32 inputs
-  float special;    // sum of the non-finite fp16 inputs (inf/NaN semantics)
-};
-
-__device__ __forceinline__ void acc_add_fp16(Acc& a, uint16_t u) {
-  const int e = (u >> 10) & 31;
-  const int m = u & 1023;
-  if (e == 31) {
-    a.special += Fp16::to_float(u);
-    return;
-  }
-  long long mag = e == 0 ? static_cast<long long>(m)
-                         : static_cast<long long>(1024 + m) << (e - 1);
-  a.fixed += (u & 0x8000u) ? -mag : mag;
-}
-
-__device__ __forceinline__ void acc_merge(Acc& a, const Acc& b) {
-  a.fixed += b.fixed;
-  a.wide += b.wide;
-  a.special += b.special;
-}
-
-__device__ __forceinline__ float acc_result(const Acc& a, bool fp16) {
-  if (!fp16) return static_cast<float>(a.wide);
-  if (a.special != 0.f || a.special != a.special) return a.special;
-  return static_cast<float>(a.fixed) * 0x1p-24f;
-}
-
-__device__ __forceinline__ void acc_load(Acc& a, const MtsParams& p, int64_t idx) {
-  if (p.fp16)
-    acc_add_fp16(a, static_cast<const uint16_t*>(p.map)[idx]);
-  else
-    a.wide += static_cast<double>(static_cast<const float*>(p.map)[idx]);
-}
-
 __global__ __launch_bounds__(kMtsThreads) void mts_kernel(MtsParams p) {
-  __shared__ long long s_fixed[kMtsThreads];
   __shared__ double s_wide[kMtsThreads];
-  __shared__ float s_special[kMtsThreads];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -89,7 +46,7 @@ __global__ __launch_bounds__(kMtsThreads) void mts_kernel(MtsParams p) {
   const int F = 3 * n;
 
   int role_id = blockIdx.x;
-  Acc acc{0, 0.0, 0.f};
+  double acc = 0.0;
 
   if (role_id < p.heads * p.n_bands) {
     // ---- diagonal band ----
@@ -106,19 +63,14 @@ __global__ __launch_bounds__(kMtsThreads) void mts_kernel(MtsParams p) {
 #pragma unroll 4
       for (int r = r_lo + wave; r < r_hi; r += 4) {
         const int c = r + off;
-        if (c >= 0 && c < n) acc_load(acc, p, base + static_cast<int64_t>(r) * n + c);
+        if (c >= 0 && c < n) acc += static_cast<double>(p.map[base + static_cast<int64_t>(r) * n + c]);
       }
     }
-    s_fixed[tid] = acc.fixed;
-    s_wide[tid] = acc.wide;
-    s_special[tid] = acc.special;
+    s_wide[tid] = acc;
     __syncthreads();
     if (wave == 0 && dk < nd) {
-      for (int w = 1; w < 4; ++w) {
-        Acc o{s_fixed[w * 64 + lane], s_wide[w * 64 + lane], s_special[w * 64 + lane]};
-        acc_merge(acc, o);
-      }
-      p.out[static_cast<int64_t>(h) * F + dk] = acc_result(acc, p.fp16);
+      for (int w = 1; w < 4; ++w) acc += s_wide[w * 64 + lane];
+      p.out[static_cast<int64_t>(h) * F + dk] = static_cast<float>(acc);
     }
     return;
   }
@@ -132,18 +84,13 @@ __global__ __launch_bounds__(kMtsThreads) void mts_kernel(MtsParams p) {
     const int64_t base = static_cast<int64_t>(h) * n * n;
     if (c < n) {
 #pragma unroll 4
-      for (int r = wave; r < n; r += 4) acc_load(acc, p, base + static_cast<int64_t>(r) * n + c);
+      for (int r = wave; r < n; r += 4) acc += static_cast<double>(p.map[base + static_cast<int64_t>(r) * n + c]);
     }
-    s_fixed[tid] = acc.fixed;
-    s_wide[tid] = acc.wide;
-    s_special[tid] = acc.special;
+    s_wide[tid] = acc;
     __syncthreads();
     if (wave == 0 && c < n) {
-      for (int w = 1; w < 4; ++w) {
-        Acc o{s_fixed[w * 64 + lane], s_wide[w * 64 + lane], s_special[w * 64 + lane]};
-        acc_merge(acc, o);
-      }
-      p.out[static_cast<int64_t>(h) * F + nd + c] = acc_result(acc, p.fp16);
+      for (int w = 1; w < 4; ++w) acc += s_wide[w * 64 + lane];
+      p.out[static_cast<int64_t>(h) * F + nd + c] = static_cast<float>(acc);
     }
     return;
   }
@@ -161,23 +108,173 @@ __global__ __launch_bounds__(kMtsThreads) void mts_kernel(MtsParams p) {
     const int rem = static_cast<int>(idx % per);
     const int i = rem / bpf;
     const int j = rem % bpf;
-    acc_load(acc, p, base + static_cast<int64_t>(f * bpf + i) * n + (f * bpf + j));
+    acc += static_cast<double>(p.map[base + static_cast<int64_t>(f * bpf + i) * n + (f * bpf + j)]);
   }
-  s_fixed[tid] = acc.fixed;
-  s_wide[tid] = acc.wide;
-  s_special[tid] = acc.special;
+  s_wide[tid] = acc;
   __syncthreads();
   for (int s = kMtsThreads / 2; s > 0; s >>= 1) {
-    if (tid < s) {
-      s_fixed[tid] += s_fixed[tid + s];
-      s_wide[tid] += s_wide[tid + s];
-      s_special[tid] += s_special[tid + s];
-    }
+    if (tid < s) s_wide[tid] += s_wide[tid + s];
     __syncthreads();
   }
+  if (tid == 0) p.out[static_cast<int64_t>(h) * F + F - 1] = static_cast<float>(s_wide[0]);
+}
+
+// -------------------------------------------------------------------------------------
+// Single pass over an fp16 map (the product path). One workgroup per (head, 64-row
+// block) reads its rows once with 16-byte loads; each thread owns 8 consecutive columns
+// and, per 16-row sub-block, keeps the column sums of its cells and the sums of the 23
+// diagonals its 8 x 16 cells lie on in fp64 registers. Every finite fp16 value is a
+// multiple of 2^-24 below 2^16, so any sum of at most 64 of them (one workgroup's share of
+// a column or a diagonal) needs at most 46 significant bits and is exact in fp64 in any
+// order. Neighbouring threads' diagonal partials overlap and are combined in LDS (fp64
+// atomics, still exact), and each workgroup adds its column, diagonal and frame-block
+// partials into an int64 accumulator per output (units of 2^-24) with global integer
+// atomics: exact and order-independent, so every output is the correctly rounded fp32 of
+// the exact sum in any workgroup order (deterministic), and the map is read once
+// (155.5 MB at the headline). A partial that is not finite (inf/NaN inputs) goes into a
+// float side accumulator instead (inf/NaN semantics only, also order-independent).
+constexpr int kMts1Threads = 256;
+constexpr int kMts1Rows = 64;  // rows per workgroup: at most 64 cells of a line per partial
+constexpr int kMts1Sub = 16;   // rows per register sub-block
+constexpr int kMts1Cols = 8;   // columns per thread
+constexpr int kMts1Diag = kMts1Cols + kMts1Sub - 1;
+constexpr int kMts1MaxN = 8192;  // LDS: n + 63 fp64 diagonal partials (66 KB)
+
+struct Mts1Params {
+  const uint16_t* map;
+  int heads;
+  int n;
+  int bpf;
+  int n_rblk;
+  unsigned long long* acc;  // (H, 3n) int64 units of 2^-24 (two's complement)
+  float* special;           // (H, 3n) sums of the non-finite partials
+  float* out;               // (H, 3n)
+};
+
+// Adds an exact fp64 partial (a multiple of 2^-24, |x| < 2^29) to an output.
+__device__ __forceinline__ void mts1_flush(const Mts1Params& p, int64_t idx, double x) {
+  if (x == 0.0) return;
+  if (__builtin_isfinite(x)) {
+    atomicAdd(&p.acc[idx], static_cast<unsigned long long>(static_cast<long long>(x * 0x1p24)));
+  } else {
+    atomicAdd(&p.special[idx], static_cast<float>(x));
+  }
+}
+
+__global__ void mts1_zero_kernel(Mts1Params p) {
+  const int64_t total = static_cast<int64_t>(p.heads) * 3 * p.n;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    p.acc[i] = 0ull;
+    p.special[i] = 0.f;
+  }
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(kMts1Threads) void mts1_kernel(Mts1Params p) {
+  extern __shared__ __align__(16) double mts1_diag[];  // n + 63 diagonals
+  __shared__ long long s_frame[kMts1Threads / 64];
+  const int tid = threadIdx.x;
+  const int h = blockIdx.x / p.n_rblk;
+  const int rb = blockIdx.x % p.n_rblk;
+  const int n = p.n;
+  const int nd = 2 * n - 1;
+  const int64_t F = 3 * static_cast<int64_t>(n);
+  const int r0 = rb * kMts1Rows;
+  const int rows = n - r0 < kMts1Rows ? n - r0 : kMts1Rows;
+  const int ndl = n + kMts1Rows - 1;  // local diagonal index kl = c - (r - r0) + 63
+  const int frame_end = (n / p.bpf) * p.bpf;
+  for (int i = tid; i < ndl; i += kMts1Threads) mts1_diag[i] = 0.0;
+  __syncthreads();
+  const uint16_t* base = p.map + (static_cast<int64_t>(h) * n + r0) * n;
+  const int64_t out0 = static_cast<int64_t>(h) * F;
+  double fsum = 0.0;
+  for (int cb = 0; cb < n; cb += kMts1Threads * kMts1Cols) {
+    const int c0 = cb + tid * kMts1Cols;
+    double cacc[kMts1Cols];
+    int cframe[kMts1Cols];  // frame of each owned column (-1 outside the frame blocks)
+#pragma unroll
+    for (int j = 0; j < kMts1Cols; ++j) {
+      cacc[j] = 0.0;
+      cframe[j] = c0 + j < frame_end ? (c0 + j) / p.bpf : -1;
+    }
+    for (int s0 = 0; s0 < rows; s0 += kMts1Sub) {
+      double dacc[kMts1Diag];
+#pragma unroll
+      for (int d = 0; d < kMts1Diag; ++d) dacc[d] = 0.0;
+      if (c0 < n) {
+#pragma unroll
+        for (int rr = 0; rr < kMts1Sub; ++rr) {
+          const int rl = s0 + rr;  // row within the block
+          if (rl < rows) {
+            const uint16_t* row = base + static_cast<int64_t>(rl) * n;
+            uint16_t v[kMts1Cols];
+            if constexpr (kVec) {
+              const u32x4 w = *reinterpret_cast<const u32x4*>(row + c0);
+#pragma unroll
+              for (int j = 0; j < kMts1Cols; ++j) v[j] = u16_at(w, j);
+            } else {
+#pragma unroll
+              for (int j = 0; j < kMts1Cols; ++j) v[j] = c0 + j < n ? row[c0 + j] : 0;
+            }
+            const int r = r0 + rl;
+            const int rframe = r < frame_end ? r / p.bpf : -2;
+            double fr = 0.0;
+#pragma unroll
+            for (int j = 0; j < kMts1Cols; ++j) {
+              const double x = static_cast<double>(Fp16::to_float(v[j]));
+              cacc[j] += x;
+              dacc[j - rr + kMts1Sub - 1] += x;
+              if (cframe[j] == rframe) fr += x;
+            }
+            fsum += fr;
+          }
+        }
+        // local diagonal of accumulator d: kl = c0 + d - 15 - s0 + 63
+#pragma unroll
+        for (int d = 0; d < kMts1Diag; ++d) {
+          const int kl = c0 + d - (kMts1Sub - 1) - s0 + (kMts1Rows - 1);
+          if (dacc[d] != 0.0 && kl >= 0 && kl < ndl) atomicAdd(&mts1_diag[kl], dacc[d]);
+        }
+      }
+    }
+    if (c0 < n) {
+#pragma unroll
+      for (int j = 0; j < kMts1Cols; ++j)
+        if (c0 + j < n) mts1_flush(p, out0 + nd + c0 + j, cacc[j]);
+    }
+  }
+  // frame-block partial of the workgroup: each thread's sum (at most 32 x 64 cells) is
+  // exact in fp64 and converts exactly to int64 units; the workgroup adds them as integers
+  long long fq = 0;
+  if (__builtin_isfinite(fsum))
+    fq = static_cast<long long>(fsum * 0x1p24);
+  else
+    atomicAdd(&p.special[out0 + F - 1], static_cast<float>(fsum));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) fq += __shfl_xor(fq, o);
+  if ((tid & 63) == 0) s_frame[tid >> 6] = fq;
+  __syncthreads();
   if (tid == 0) {
-    Acc tot{s_fixed[0], s_wide[0], s_special[0]};
-    p.out[static_cast<int64_t>(h) * F + F - 1] = acc_result(tot, p.fp16);
+    long long t = 0;
+    for (int w = 0; w < kMts1Threads / 64; ++w) t += s_frame[w];
+    if (t != 0) atomicAdd(&p.acc[out0 + F - 1], static_cast<unsigned long long>(t));
+  }
+  // diagonal partials: global index k = kl + n - 64 - r0
+  for (int kl = tid; kl < ndl; kl += kMts1Threads) {
+    const int k = kl + n - kMts1Rows - r0;
+    if (k >= 0 && k < nd) mts1_flush(p, out0 + k, mts1_diag[kl]);
+  }
+}
+
+__global__ void mts1_finalize_kernel(Mts1Params p) {
+  const int64_t total = static_cast<int64_t>(p.heads) * 3 * p.n;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const float sp = p.special[i];
+    p.out[i] = (sp != 0.f || sp != sp)
+                   ? sp
+                   : static_cast<float>(static_cast<long long>(p.acc[i])) * 0x1p-24f;
   }
 }
 
@@ -375,12 +472,10 @@ struct MaskParams {
   int kv_tiles;            // key tiles at or beyond are dropped (from_mask only)
 };
 
-__device__ __forceinline__ bool video_cell(const uint8_t* colsel, const uint8_t* diagsel,
-                                           int mode, int n, int bpf, int i, int j) {
-  if (mode == MODDIT_MODE_FULL) return true;
-  if (colsel[j] | diagsel[j - i + n - 1]) return true;
-  return mode == MODDIT_MODE_BLOCK_DIAGONAL && (i / bpf) == (j / bpf);
-}
+// Tiles per workgroup: the selected-line byte maps are built in LDS once per workgroup
+// and serve this many consecutive query tiles of the head.
+constexpr int kMaskTilesPerWg = 8;
+constexpr int kMaskCols = 8;  // mask columns per thread and pass
 
 template <bool kFromMask>
 __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) {
@@ -391,8 +486,10 @@ __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) 
   __shared__ int s_total;
 
   const int tid = threadIdx.x;
-  const int h = blockIdx.x / p.n_qtiles;
-  const int t = blockIdx.x % p.n_qtiles;
+  const int wg_per_head = (p.n_qtiles + kMaskTilesPerWg - 1) / kMaskTilesPerWg;
+  const int h = blockIdx.x / wg_per_head;
+  const int t_begin = (blockIdx.x % wg_per_head) * kMaskTilesPerWg;
+  const int t_end = t_begin + kMaskTilesPerWg < p.n_qtiles ? t_begin + kMaskTilesPerWg : p.n_qtiles;
   const int n = p.n;
   const int nb = p.nb;
   int mode = 0;
@@ -409,94 +506,130 @@ __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) 
     }
     __syncthreads();
   }
-
-  // Mask rows covered by this query tile.
-  const int rows_per_tile = p.block == 64 ? 2 : 1;
-  const int r0 = t * rows_per_tile;
-  const int r1 = r0 + 1;
-  const int n_rows = p.n_rows;
-  const bool has_r1 = rows_per_tile == 2 && r1 < n_rows;
-
-  auto cell = [&](int i, int j) -> bool {
-    if (kFromMask) return p.mask_in[h * p.in_head_stride + i * p.in_row_stride + j] != 0;
+  // Video block index of mask row/column q (-1 outside the video: all-true text rows and
+  // columns of the hunyuan / cogvideox layouts; every cell of the 'other' layout).
+  auto video_index = [&](int q) -> int {
     switch (p.layout) {
-      case MODDIT_LAYOUT_WAN:
-        return video_cell(colsel, diagsel, mode, n, p.bpf, i, j);
-      case MODDIT_LAYOUT_HUNYUAN:
-        if (i < n && j < n) return video_cell(colsel, diagsel, mode, n, p.bpf, i, j);
-        return true;
-      case MODDIT_LAYOUT_COGVIDEOX: {
-        const int tb = p.text_blocks;
-        if (i >= tb && j >= tb) return video_cell(colsel, diagsel, mode, n, p.bpf, i - tb, j - tb);
-        return true;
-      }
-      default:
-        return true;
+      case MODDIT_LAYOUT_WAN: return q;
+      case MODDIT_LAYOUT_HUNYUAN: return q < n ? q : -1;
+      case MODDIT_LAYOUT_COGVIDEOX: return q >= p.text_blocks ? q - p.text_blocks : -1;
+      default: return -1;
     }
   };
-
-  const int chunk = (nb + kMaskThreads - 1) / kMaskThreads;
-  const int j0 = tid * chunk;
-  const int j1 = j0 + chunk < nb ? j0 + chunk : nb;
+  const bool full = mode == MODDIT_MODE_FULL;
+  const bool bd = mode == MODDIT_MODE_BLOCK_DIAGONAL;
+  const int rows_per_tile = p.block == 64 ? 2 : 1;
   const int tiles_per_col = p.block == 64 ? 1 : 2;
+  const int n_rows = p.n_rows;
+  const bool vec_mask = (nb % kMaskCols) == 0 && p.mask_out != nullptr &&
+                        (reinterpret_cast<uintptr_t>(p.mask_out) & 7) == 0;
 
-  // pass 1: mask bytes + entry count
-  int cnt = 0;
-  for (int j = j0; j < j1; ++j) {
-    const bool m0 = r0 < n_rows && cell(r0, j);
-    const bool m1 = has_r1 && cell(r1, j);
-    if (!kFromMask && p.mask_out) {
-      if (r0 < n_rows) p.mask_out[(static_cast<int64_t>(h) * nb + r0) * nb + j] = m0;
-      if (has_r1) p.mask_out[(static_cast<int64_t>(h) * nb + r1) * nb + j] = m1;
-    }
-    if (m0 || m1) {
-      for (int s = 0; s < tiles_per_col; ++s)
-        if (j * tiles_per_col + s < p.kv_tiles) ++cnt;
-    }
-  }
-  if (p.counts == nullptr) return;
-
-  // block exclusive scan of cnt (256 threads = 4 waves)
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  int incl = cnt;
+  for (int t = t_begin; t < t_end; ++t) {
+    const int r0 = t * rows_per_tile;
+    const int r1 = r0 + 1;
+    const bool has_r0 = r0 < n_rows;
+    const bool has_r1 = rows_per_tile == 2 && r1 < n_rows;
+    const int iv0 = kFromMask ? 0 : video_index(r0);
+    const int iv1 = kFromMask ? 0 : video_index(r1);
+    const int if0 = iv0 >= 0 ? iv0 / p.bpf : -2;
+    const int if1 = iv1 >= 0 ? iv1 / p.bpf : -2;
+    const int64_t slot = static_cast<int64_t>(h) * p.n_qtiles + t;
+    int32_t* out = p.counts ? p.entries + slot * p.cap : nullptr;
+    int written = 0;
+    for (int jb = 0; jb < nb; jb += kMaskThreads * kMaskCols) {
+      const int j0 = jb + tid * kMaskCols;
+      unsigned m0 = 0, m1 = 0;  // bit c: column j0 + c is active in row r0 / r1
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int v = __shfl_up(incl, o);
-    if (lane >= o) incl += v;
-  }
-  if (lane == 63) s_wave[wave] = incl;
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int w = 0; w < kMaskThreads / 64; ++w) {
-      const int v = s_wave[w];
-      s_wave[w] = run;
-      run += v;
-    }
-    s_total = run;
-  }
-  __syncthreads();
-  int pos = s_wave[wave] + incl - cnt;
-
-  const int64_t slot = static_cast<int64_t>(h) * p.n_qtiles + t;
-  int32_t* out = p.entries + slot * p.cap;
-  for (int j = j0; j < j1; ++j) {
-    const bool m0 = r0 < n_rows && cell(r0, j);
-    const bool m1 = has_r1 && cell(r1, j);
-    if (!(m0 || m1)) continue;
-    int bits;
-    if (p.block == 128 || p.union_rows) bits = 3;
-    else bits = (m0 ? 1 : 0) | (m1 ? 2 : 0);
-    for (int s = 0; s < tiles_per_col; ++s) {
-      const int kt = j * tiles_per_col + s;
-      if (kt < p.kv_tiles) {
-        if (pos < p.cap) out[pos] = (kt << 2) | bits;
-        ++pos;
+      for (int c = 0; c < kMaskCols; ++c) {
+        const int j = j0 + c;
+        if (j >= nb) break;
+        bool a0, a1;
+        if (kFromMask) {
+          const uint8_t* col = p.mask_in + h * p.in_head_stride + j;
+          a0 = has_r0 && col[r0 * p.in_row_stride] != 0;
+          a1 = has_r1 && col[r1 * p.in_row_stride] != 0;
+        } else {
+          const int jv = video_index(j);
+          const int jf = jv >= 0 ? jv / p.bpf : -3;
+          const bool colj = jv >= 0 && colsel[jv];
+          a0 = has_r0 && (iv0 < 0 || jv < 0 || full || colj || diagsel[jv - iv0 + n - 1] ||
+                          (bd && if0 == jf));
+          a1 = has_r1 && (iv1 < 0 || jv < 0 || full || colj || diagsel[jv - iv1 + n - 1] ||
+                          (bd && if1 == jf));
+        }
+        m0 |= static_cast<unsigned>(a0) << c;
+        m1 |= static_cast<unsigned>(a1) << c;
       }
+      if (!kFromMask && p.mask_out && j0 < nb) {
+        uint8_t* row0 = p.mask_out + (static_cast<int64_t>(h) * nb + r0) * nb + j0;
+        if (vec_mask) {
+          uint64_t b0 = 0, b1 = 0;  // bit c -> byte c (0/1)
+#pragma unroll
+          for (int c = 0; c < kMaskCols; ++c) {
+            b0 |= static_cast<uint64_t>((m0 >> c) & 1u) << (8 * c);
+            b1 |= static_cast<uint64_t>((m1 >> c) & 1u) << (8 * c);
+          }
+          if (has_r0) *reinterpret_cast<uint64_t*>(row0) = b0;
+          if (has_r1) *reinterpret_cast<uint64_t*>(row0 + nb) = b1;
+        } else {
+          for (int c = 0; c < kMaskCols && j0 + c < nb; ++c) {
+            if (has_r0) row0[c] = (m0 >> c) & 1;
+            if (has_r1) row0[nb + c] = (m1 >> c) & 1;
+          }
+        }
+      }
+      if (out == nullptr) continue;
+      // entries: ascending key tiles, counted then placed by an ordered block scan
+      int cnt = 0;
+      const unsigned any = m0 | m1;
+#pragma unroll
+      for (int c = 0; c < kMaskCols; ++c) {
+        if ((any >> c) & 1) {
+          for (int s2 = 0; s2 < tiles_per_col; ++s2)
+            if ((j0 + c) * tiles_per_col + s2 < p.kv_tiles) ++cnt;
+        }
+      }
+      const int lane = tid & 63;
+      const int wave = tid >> 6;
+      int incl = cnt;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+      }
+      if (lane == 63) s_wave[wave] = incl;
+      __syncthreads();
+      if (tid == 0) {
+        int run = 0;
+        for (int w = 0; w < kMaskThreads / 64; ++w) {
+          const int v = s_wave[w];
+          s_wave[w] = run;
+          run += v;
+        }
+        s_total = run;
+      }
+      __syncthreads();
+      int pos = written + s_wave[wave] + incl - cnt;
+      const int total = s_total;
+      __syncthreads();  // s_wave / s_total are rewritten by the next pass
+#pragma unroll
+      for (int c = 0; c < kMaskCols; ++c) {
+        if (!((any >> c) & 1)) continue;
+        int bits;
+        if (p.block == 128 || p.union_rows) bits = 3;
+        else bits = static_cast<int>((m0 >> c) & 1) | (static_cast<int>((m1 >> c) & 1) << 1);
+        for (int s2 = 0; s2 < tiles_per_col; ++s2) {
+          const int kt = (j0 + c) * tiles_per_col + s2;
+          if (kt < p.kv_tiles) {
+            if (pos < p.cap) out[pos] = (kt << 2) | bits;
+            ++pos;
+          }
+        }
+      }
+      written += total;
     }
+    if (out != nullptr && tid == 0) p.counts[slot] = written < p.cap ? written : p.cap;
   }
-  if (tid == 0) p.counts[slot] = s_total < p.cap ? s_total : p.cap;
 }
 
 // =====================================================================================
@@ -523,8 +656,13 @@ __global__ void refresh_merge_kernel(const uint16_t* __restrict__ prev,
 
 using namespace moddit;
 
+extern "C" int64_t moddit_mts_workspace_bytes(int heads, int n) {
+  if (heads <= 0 || n <= 0) return 0;
+  return static_cast<int64_t>(heads) * 3 * n * (sizeof(unsigned long long) + sizeof(float));
+}
+
 extern "C" int moddit_mts(const void* map, int map_dtype, int heads, int n, int blocks_per_frame,
-                          float* mts_out, moddit_stream_t stream) {
+                          void* workspace, float* mts_out, moddit_stream_t stream) {
   clear_error();
   MODDIT_CHECK_ARG(map && mts_out, "mts: null pointer argument");
   MODDIT_CHECK_ARG(map_dtype == MODDIT_FP16 || map_dtype == MODDIT_FP32,
@@ -533,9 +671,45 @@ extern "C" int moddit_mts(const void* map, int map_dtype, int heads, int n, int 
   MODDIT_CHECK_ARG(blocks_per_frame > 0, "mts: blocks_per_frame must be positive, got %d",
                    blocks_per_frame);
   if (heads == 0) return MODDIT_OK;
+  hipStream_t st = as_stream(stream);
+  if (map_dtype == MODDIT_FP16) {
+    MODDIT_CHECK_ARG(workspace != nullptr, "mts: fp16 maps need a workspace of "
+                     "moddit_mts_workspace_bytes(heads, n) bytes");
+    MODDIT_CHECK_ARG(aligned16(workspace), "mts: workspace must be 16-byte aligned");
+    MODDIT_CHECK_ARG(n <= kMts1MaxN, "mts: n=%d exceeds %d", n, kMts1MaxN);
+    Mts1Params q;
+    q.map = static_cast<const uint16_t*>(map);
+    q.heads = heads;
+    q.n = n;
+    q.bpf = blocks_per_frame;
+    q.n_rblk = (n + kMts1Rows - 1) / kMts1Rows;
+    const int64_t total = static_cast<int64_t>(heads) * 3 * n;
+    q.acc = static_cast<unsigned long long*>(workspace);
+    q.special = reinterpret_cast<float*>(q.acc + total);
+    q.out = mts_out;
+    const int64_t grid = static_cast<int64_t>(heads) * q.n_rblk;
+    MODDIT_CHECK_ARG(grid < 0x7fffffff, "mts: shape too large");
+    int64_t fill = (total + 255) / 256;
+    if (fill > 4096) fill = 4096;
+    hipLaunchKernelGGL(mts1_zero_kernel, dim3(static_cast<unsigned>(fill)), dim3(256), 0, st, q);
+    MODDIT_CHECK_LAUNCH("mts (zero)");
+    const size_t lds = static_cast<size_t>(n + kMts1Rows - 1) * sizeof(double);
+    static LaunchSetup once_vec, once_scalar;
+    const bool vec = n % 8 == 0 && aligned16(map);
+    auto kernel = vec ? mts1_kernel<true> : mts1_kernel<false>;
+    if (set_dynamic_lds_once(vec ? once_vec : once_scalar, reinterpret_cast<const void*>(kernel),
+                             (kMts1MaxN + kMts1Rows - 1) * 8) != hipSuccess) {
+      set_error("mts: cannot reserve LDS");
+      return MODDIT_EHIP;
+    }
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(kMts1Threads), lds, st, q);
+    MODDIT_CHECK_LAUNCH("mts");
+    hipLaunchKernelGGL(mts1_finalize_kernel, dim3(static_cast<unsigned>(fill)), dim3(256), 0, st, q);
+    MODDIT_CHECK_LAUNCH("mts (finalize)");
+    return MODDIT_OK;
+  }
   MtsParams p;
-  p.map = map;
-  p.fp16 = map_dtype == MODDIT_FP16;
+  p.map = static_cast<const float*>(map);
   p.heads = heads;
   p.n = n;
   p.bpf = blocks_per_frame;
@@ -544,8 +718,7 @@ extern "C" int moddit_mts(const void* map, int map_dtype, int heads, int n, int 
   p.out = mts_out;
   const int64_t grid = static_cast<int64_t>(heads) * (p.n_bands + p.n_strips + 1);
   MODDIT_CHECK_ARG(grid < 0x7fffffff, "mts: shape too large");
-  hipLaunchKernelGGL(mts_kernel, dim3(static_cast<unsigned>(grid)), dim3(kMtsThreads), 0,
-                     as_stream(stream), p);
+  hipLaunchKernelGGL(mts_kernel, dim3(static_cast<unsigned>(grid)), dim3(kMtsThreads), 0, st, p);
   MODDIT_CHECK_LAUNCH("mts");
   return MODDIT_OK;
 }
@@ -681,7 +854,7 @@ extern "C" int moddit_mask_from_lines(const int32_t* sel, int heads, int k, cons
   p.kv_tiles = 0x7fffffff;
   const size_t lds = static_cast<size_t>(3 * n);
   MODDIT_CHECK_ARG(lds <= 65536, "mask_from_lines: n=%d too large", n);
-  const int64_t grid = static_cast<int64_t>(heads) * n_qtiles;
+  const int64_t grid = static_cast<int64_t>(heads) * ((n_qtiles + kMaskTilesPerWg - 1) / kMaskTilesPerWg);
   hipLaunchKernelGGL(mask_tiles_kernel<false>, dim3(static_cast<unsigned>(grid)),
                      dim3(kMaskThreads), lds, as_stream(stream), p);
   MODDIT_CHECK_LAUNCH("mask_from_lines");
@@ -717,7 +890,7 @@ extern "C" int moddit_mask_to_tiles(const uint8_t* mask, int heads, int n_rows, 
   p.n_qtiles = n_qtiles;
   p.cap = cap;
   p.kv_tiles = kv_tiles < 0 ? 0 : kv_tiles;
-  const int64_t grid = static_cast<int64_t>(heads) * n_qtiles;
+  const int64_t grid = static_cast<int64_t>(heads) * ((n_qtiles + kMaskTilesPerWg - 1) / kMaskTilesPerWg);
   hipLaunchKernelGGL(mask_tiles_kernel<true>, dim3(static_cast<unsigned>(grid)),
                      dim3(kMaskThreads), 16, as_stream(stream), p);
   MODDIT_CHECK_LAUNCH("mask_to_tiles");

@@ -314,9 +314,13 @@ def compute_mts(S_T: torch.Tensor, blocks_per_frame: int) -> torch.Tensor:
         raise TypeError(f"S_T must be float16 or float32, got {S_T.dtype}")
     S_T = S_T.contiguous()
     H, n, _ = S_T.shape
+    lib = _lib.load()
     out = torch.empty((H, 3 * n), device=S_T.device, dtype=torch.float32)
-    check(_lib.load().moddit_mts(S_T.data_ptr(), dt, H, n, int(blocks_per_frame), out.data_ptr(),
-                                 _stream(S_T)), "moddit_mts")
+    ws = None
+    if dt == _lib.FP16 and H > 0:
+        ws = torch.empty(lib.moddit_mts_workspace_bytes(H, n), device=S_T.device, dtype=torch.uint8)
+    check(lib.moddit_mts(S_T.data_ptr(), dt, H, n, int(blocks_per_frame), _ptr(ws),
+                         out.data_ptr(), _stream(S_T)), "moddit_mts")
     return out
 
 

@@ -421,14 +421,51 @@ def test_mts_bit_exact_on_map_domain(n, bpf):
         assert np.array_equal(got[:, :-1], loop[:, :-1])
 
 
-def test_mts_arbitrary_fp16_and_fp32_inputs():
-    rng = np.random.default_rng(3)
-    n, bpf = 37, 5
-    bits = rng.integers(0, 0x7C00, size=(2, n, n)).astype(np.uint16)
+@pytest.mark.parametrize("n,bpf,H", [(37, 5, 2), (120, 9, 2), (2112, 64, 1)])
+def test_mts_arbitrary_fp16_inputs(n, bpf, H):
+    """Any finite fp16 (both signs, subnormals, up to 65504): exact sums rounded once.
+    n=37: the scalar-load path; n=120: 16-byte loads; n=2112: two column chunks per
+    workgroup (each thread owns 8 columns of 2048 per chunk)."""
+    rng = np.random.default_rng(n)
+    bits = rng.integers(0, 0x7C00, size=(H, n, n)).astype(np.uint16)
     bits |= (rng.integers(0, 2, size=bits.shape) << 15).astype(np.uint16)
     S = bits.view(np.float16)
-    got = md.compute_mts(torch.from_numpy(S.copy()).to(DEV), bpf).cpu().numpy()
+    t = torch.from_numpy(S.copy()).to(DEV)
+    got = md.compute_mts(t, bpf).cpu().numpy()
     assert np.array_equal(got, O.mts_exact(S, bpf))
+    assert np.array_equal(md.compute_mts(t, bpf).cpu().numpy(), got)  # deterministic
+
+
+def test_mts_non_finite_fp16_inputs_follow_float_semantics():
+    """An output whose cells hold inf/NaN is the float sum of those values (NaN if a NaN
+    or both infinities occur); the other outputs stay exact."""
+    rng = np.random.default_rng(11)
+    n, bpf = 48, 8
+    S = (rng.integers(0, 4097, size=(1, n, n)) / 4096.0).astype(np.float16)
+    S[0, 3, 5] = np.inf      # column 5, diagonal 2
+    S[0, 7, 9] = -np.inf     # column 9, diagonal 2 as well -> NaN there
+    S[0, 10, 10] = np.inf    # column 10, main diagonal, frame block 1
+    S[0, 20, 40] = np.nan    # column 40, diagonal 20
+    got = md.compute_mts(torch.from_numpy(S).to(DEV), bpf).cpu().numpy()[0]
+    finite = np.where(np.isfinite(S), S, np.float16(0))
+    want = O.mts_exact(finite, bpf)[0]
+    nd = 2 * n - 1
+    special = np.zeros(3 * n)
+    for (r, c) in zip(*np.nonzero(~np.isfinite(S[0]))):
+        v = float(S[0, r, c])
+        idx = [nd + c, c - r + n - 1]
+        if r // bpf == c // bpf:
+            idx.append(3 * n - 1)
+        for i in idx:
+            special[i] = v if special[i] == 0 else special[i] + v
+    want = np.where((special != 0) | np.isnan(special), special, want).astype(np.float32)
+    np.testing.assert_array_equal(got, want)
+    assert np.isnan(got[nd + 40]) and np.isnan(got[2 + n - 1])  # NaN cell; inf + -inf
+
+
+def test_mts_fp32_inputs():
+    rng = np.random.default_rng(3)
+    n, bpf = 37, 5
     S32 = rng.normal(size=(2, n, n)).astype(np.float32)
     got32 = md.compute_mts(torch.from_numpy(S32).to(DEV), bpf).cpu().numpy()
     want = np.stack([O.moddit_ref._mts_f64(S32[h].astype(np.float64), bpf) for h in range(2)])
