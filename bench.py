@@ -698,7 +698,9 @@ def main(argv=None):
     achieved = exec_flop / (kernel_ms * 1e-3) / 1e12
     traffic, traffic_src = measured_traffic() if args.config == "hunyuan" else (None, None)
     result = {
-        "metric": "block-sparse attn effective TFLOP/s + ms/call at 115k tokens, 83% sparsity",
+        "metric": ("block-sparse attn effective TFLOP/s + ms/call at 115k tokens, 83% sparsity"
+                   if args.config == "hunyuan" else
+                   f"block-sparse attn effective TFLOP/s + ms/call, {args.config} configuration"),
         "value": round(eff_flop / (ms * 1e-3) / 1e12, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
