@@ -20,6 +20,7 @@ and tiles and reported under "q8" (a reported alternative; the headline stays bf
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -154,6 +155,32 @@ def measured_traffic(name="attention_hunyuan_headline.md"):
     except OSError:
         pass
     return None, None
+
+
+def mfma_ceiling(kind, iters=4000, reps=3, zeros=False):
+    """MFMA rate and shader clock on random operands, from the calibration library built
+    next to libmoddit.so (mod-dit_amd/csrc/calib/mfma_ceiling.hip): back-to-back MFMAs
+    only, two waves per SIMD, one 8-wave workgroup per CU. kind 0: bf16 32x32x16, 1: int8
+    32x32x32, 2: fp8 e4m3 32x32x64. Under sustained MFMA load the clock settles at the
+    board's power limit, so this is the rate the published peak shrinks to on real data.
+    `zeros` runs the same loop on all-zero operands (for contrast: those draw less power).
+    Returns None when the library is missing or the measurement fails."""
+    path = os.path.join(ROOT, "mod-dit_amd", "libmoddit_calib.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    fn = lib.moddit_calib_mfma
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_double)] * 3
+    torch.cuda.synchronize()
+    rate, mhz, cyc = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    if fn(kind, int(zeros), iters, reps, ctypes.byref(rate), ctypes.byref(mhz), ctypes.byref(cyc)) != 0:
+        return None
+    names = ("v_mfma_f32_32x32x16_bf16", "v_mfma_i32_32x32x32_i8",
+             "v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3)")
+    return {"value": round(rate.value, 1), "unit": "TOP/s" if kind == 1 else "TFLOP/s",
+            "clock_mhz": round(mhz.value), "cycles_per_mfma_per_simd": round(cyc.value, 2),
+            "mfma": names[kind], "operands": "zeros" if zeros else "random"}
 
 
 def time_events(fn, reps):
@@ -556,6 +583,9 @@ def main(argv=None):
                     default=None,
                     help="run only the named kernel(s) after setup (for rocprofv3 counter passes); "
                          "prints no JSON")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only measure the MFMA ceilings (bf16, int8, fp8; random and all-zero "
+                         "operands) and print them as one JSON line")
     args = ap.parse_args(argv)
 
     if args.precision != "bf16" and not args.sweep:
@@ -569,6 +599,13 @@ def main(argv=None):
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+
+    if args.calibrate:
+        rows = [mfma_ceiling(kind, zeros=z) for kind in (0, 1, 2) for z in (False, True)]
+        print(json.dumps({"metric": "MFMA ceiling by operand data", "published_peak": {
+            "bf16": MI355X_BF16_DENSE_TFLOPS, "int8": INT8_FP8_PEAK_TFLOPS,
+            "fp8": INT8_FP8_PEAK_TFLOPS}, "rows": rows}), flush=True)
+        return 0 if all(rows) else 1
 
     if args.profile == "copy":
         # calibration for HBM byte counters: a plain device copy of a known size
@@ -695,6 +732,16 @@ def main(argv=None):
                            T=art["T"], top_k=art["top_k"], threshold=args.threshold,
                            what=f"the {args.config}-like layer")
 
+    log("measuring the MFMA ceiling on random operands")
+    ceiling = mfma_ceiling(0)
+    if q8 is not None:
+        c8, cf8 = mfma_ceiling(1), mfma_ceiling(2)
+        q8["mfma_ceiling_int8"], q8["mfma_ceiling_fp8"] = c8, cf8
+        if c8 and cf8:
+            # Q.K^T (int8) and P.V (fp8) each carry half of the executed operations
+            mix = 1.0 / (0.5 / c8["value"] + 0.5 / cf8["value"])
+            q8["sparse_frac_of_mfma_ceiling"] = round(q8["sparse_executed_tflops"] / mix, 4)
+
     achieved = exec_flop / (kernel_ms * 1e-3) / 1e12
     traffic, traffic_src = measured_traffic() if args.config == "hunyuan" else (None, None)
     result = {
@@ -743,6 +790,8 @@ def main(argv=None):
             "traffic_source": traffic_src,
             "kernel": "attention_fwd_kernel<128, Bf16, sparse>",
             "kernel_ms": round(kernel_ms, 4),
+            "mfma_ceiling": ceiling,
+            "frac_of_mfma_ceiling": (round(achieved / ceiling["value"], 4) if ceiling else None),
         },
         "cpu_baseline": cpu,
         "q8": q8,

@@ -22,6 +22,9 @@ CSRC = PKG_DIR / "csrc"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_NAME = "libmoddit.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+# measurement aid for bench.py (MFMA ceiling on random operands); not part of the C ABI
+CALIB_SRC = CSRC / "calib" / "mfma_ceiling.hip"
+CALIB_PATH = PKG_DIR / "libmoddit_calib.so"
 
 ARCH = "gfx950"
 COMMON_FLAGS = [
@@ -57,7 +60,8 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile csrc/*.hip for gfx950 and link libmoddit.so; returns the library path."""
+    """Compile csrc/*.hip for gfx950 and link libmoddit.so (and the calibration library);
+    returns the path of libmoddit.so."""
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
@@ -75,7 +79,16 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIB_PATH)
+    build_calib(verbose)
     return LIB_PATH
+
+
+def build_calib(verbose: bool = False) -> Path:
+    """Compile the MFMA-ceiling measurement kernel into libmoddit_calib.so."""
+    tmp = CALIB_PATH.with_suffix(".so.tmp")
+    _run([hipcc(), *COMMON_FLAGS, "-shared", "-o", str(tmp), str(CALIB_SRC)], verbose)
+    os.replace(tmp, CALIB_PATH)
+    return CALIB_PATH
 
 
 def main(argv: list[str] | None = None) -> int:

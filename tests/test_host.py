@@ -30,6 +30,24 @@ def test_library_exports_every_declared_symbol():
     assert lib.moddit_version().startswith(b"moddit-mi355x")
 
 
+def test_calibration_library_stays_outside_the_c_abi():
+    """bench.py's MFMA-ceiling kernel lives in its own library: the drop-in library and
+    its header carry no calibration entry point."""
+    calib = _lib.LIB_PATH.parent / "libmoddit_calib.so"
+    assert calib.exists(), "build() builds libmoddit_calib.so next to libmoddit.so"
+    lib = ctypes.CDLL(str(calib))
+    assert hasattr(lib, "moddit_calib_mfma")
+    assert not hasattr(_lib.load(), "moddit_calib_mfma")
+    assert "moddit_calib_mfma" not in _declared_symbols()
+    fn = lib.moddit_calib_mfma
+    fn.restype = ctypes.c_int
+    d = ctypes.c_double()
+    # argument errors are reported before any HIP call
+    assert fn(3, 0, 10, 1, ctypes.byref(d), ctypes.byref(d), ctypes.byref(d)) == 2
+    assert fn(0, 0, 0, 1, ctypes.byref(d), ctypes.byref(d), ctypes.byref(d)) == 2
+    assert fn(0, 0, 10, 1, None, ctypes.byref(d), ctypes.byref(d)) == 2
+
+
 def test_mtm_host_matches_oracle_closed_form_and_brute_force():
     for n, bpf in [(4, 2), (9, 4), (64, 16)]:
         got = md.compute_mtm(n, bpf, 1.0).numpy()
