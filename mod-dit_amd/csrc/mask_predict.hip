@@ -120,38 +120,47 @@ __global__ __launch_bounds__(kMtsThreads) void mts_kernel(MtsParams p) {
 }
 
 // -------------------------------------------------------------------------------------
-// Single pass over an fp16 map (the product path). One workgroup per (head, 64-row
-// block) reads its rows once with 16-byte loads; each thread owns 8 consecutive columns
-// and, per 16-row sub-block, keeps the column sums of its cells and the sums of the 23
-// diagonals its 8 x 16 cells lie on in fp64 registers. Every finite fp16 value is a
-// multiple of 2^-24 below 2^16, so any sum of at most 64 of them (one workgroup's share of
-// a column or a diagonal) needs at most 46 significant bits and is exact in fp64 in any
-// order. Neighbouring threads' diagonal partials overlap and are combined in LDS (fp64
-// atomics, still exact), and each workgroup adds its column, diagonal and frame-block
-// partials into an int64 accumulator per output (units of 2^-24) with global integer
-// atomics: exact and order-independent, so every output is the correctly rounded fp32 of
-// the exact sum in any workgroup order (deterministic), and the map is read once
-// (155.5 MB at the headline). A partial that is not finite (inf/NaN inputs) goes into a
-// float side accumulator instead (inf/NaN semantics only, also order-independent).
+// Single pass over an fp16 map (the product path). One workgroup per (head, 512-row x
+// 256-column tile) reads its cells once with 16-byte loads. Each thread owns 8 consecutive
+// columns of one 64-row slab of the tile and keeps its column sums and, per 16-row
+// sub-block, the sums of the 23 diagonals its 8 x 16 cells lie on in fp64 registers.
+// Every finite fp16 value is a multiple of 2^-24 below 2^16, so any sum of at most 8192 of
+// them needs at most 53 significant bits and is exact in fp64 in any order; a tile's
+// share of one line is at most 512 cells. The eight slabs' column sums and the threads'
+// overlapping diagonal sums are combined in LDS (still exact), and each workgroup adds
+// its column, diagonal and frame-block partials into an int64 accumulator per output
+// (units of 2^-24) with global integer atomics: exact and order-independent, so every
+// output is the correctly rounded fp32 of the exact sum in any workgroup order
+// (deterministic), and the map is read once (155.5 MB at the headline). A partial that is
+// not finite (inf/NaN inputs) goes into a float side accumulator instead (inf/NaN
+// semantics only, also order-independent). The tile shape minimises the global atomics
+// per cell for its area (256 column + 767 diagonal partials per 131,072 cells): contended
+// atomics, not the loads, were what bounded the 64-row-block version of this pass.
 constexpr int kMts1Threads = 256;
-constexpr int kMts1Rows = 64;  // rows per workgroup: at most 64 cells of a line per partial
-constexpr int kMts1Sub = 16;   // rows per register sub-block
-constexpr int kMts1Cols = 8;   // columns per thread
-constexpr int kMts1Diag = kMts1Cols + kMts1Sub - 1;
-constexpr int kMts1MaxN = 8192;  // LDS: n + 63 fp64 diagonal partials (66 KB)
+constexpr int kMts1Cols = 8;         // columns per thread
+constexpr int kMts1Sub = 16;         // rows per register sub-block
+constexpr int kMts1Slab = 64;        // rows per thread
+constexpr int kMts1ColThreads = 32;  // threads across a tile's columns
+constexpr int kMts1Slabs = kMts1Threads / kMts1ColThreads;   // 8
+constexpr int kMts1TileC = kMts1ColThreads * kMts1Cols;      // 256
+constexpr int kMts1TileR = kMts1Slabs * kMts1Slab;           // 512
+constexpr int kMts1Diag = kMts1Cols + kMts1Sub - 1;          // 23
+constexpr int kMts1TileDiag = kMts1TileC + kMts1TileR - 1;   // 767
+constexpr int kMts1MaxN = 1 << 20;  // int64 units: |sum| <= n * 2^40 stays below 2^63
 
 struct Mts1Params {
   const uint16_t* map;
   int heads;
   int n;
   int bpf;
-  int n_rblk;
+  int n_rt;  // row tiles per head
+  int n_ct;  // column tiles per head
   unsigned long long* acc;  // (H, 3n) int64 units of 2^-24 (two's complement)
   float* special;           // (H, 3n) sums of the non-finite partials
   float* out;               // (H, 3n)
 };
 
-// Adds an exact fp64 partial (a multiple of 2^-24, |x| < 2^29) to an output.
+// Adds an exact fp64 partial (a multiple of 2^-24, |x| < 2^25) to an output.
 __device__ __forceinline__ void mts1_flush(const Mts1Params& p, int64_t idx, double x) {
   if (x == 0.0) return;
   if (__builtin_isfinite(x)) {
@@ -172,80 +181,84 @@ __global__ void mts1_zero_kernel(Mts1Params p) {
 
 template <bool kVec>
 __global__ __launch_bounds__(kMts1Threads) void mts1_kernel(Mts1Params p) {
-  extern __shared__ __align__(16) double mts1_diag[];  // n + 63 diagonals
+  __shared__ double s_diag[kMts1TileDiag];
+  __shared__ double s_col[kMts1Slabs][kMts1TileC];
   __shared__ long long s_frame[kMts1Threads / 64];
   const int tid = threadIdx.x;
-  const int h = blockIdx.x / p.n_rblk;
-  const int rb = blockIdx.x % p.n_rblk;
+  const int tc = tid % kMts1ColThreads;
+  const int tr = tid / kMts1ColThreads;
+  const int tiles = p.n_rt * p.n_ct;
+  const int h = blockIdx.x / tiles;
+  const int t = blockIdx.x - h * tiles;
+  const int R0 = (t / p.n_ct) * kMts1TileR;
+  const int C0 = (t % p.n_ct) * kMts1TileC;
   const int n = p.n;
   const int nd = 2 * n - 1;
   const int64_t F = 3 * static_cast<int64_t>(n);
-  const int r0 = rb * kMts1Rows;
-  const int rows = n - r0 < kMts1Rows ? n - r0 : kMts1Rows;
-  const int ndl = n + kMts1Rows - 1;  // local diagonal index kl = c - (r - r0) + 63
   const int frame_end = (n / p.bpf) * p.bpf;
-  for (int i = tid; i < ndl; i += kMts1Threads) mts1_diag[i] = 0.0;
+  for (int i = tid; i < kMts1TileDiag; i += kMts1Threads) s_diag[i] = 0.0;
   __syncthreads();
-  const uint16_t* base = p.map + (static_cast<int64_t>(h) * n + r0) * n;
+
+  const int c0 = C0 + tc * kMts1Cols;   // this thread's first column
+  const int rs = R0 + tr * kMts1Slab;   // this thread's first row
+  const uint16_t* base = p.map + static_cast<int64_t>(h) * n * n;
   const int64_t out0 = static_cast<int64_t>(h) * F;
-  double fsum = 0.0;
-  for (int cb = 0; cb < n; cb += kMts1Threads * kMts1Cols) {
-    const int c0 = cb + tid * kMts1Cols;
-    double cacc[kMts1Cols];
-    int cframe[kMts1Cols];  // frame of each owned column (-1 outside the frame blocks)
+  // frames of the first and last owned columns inside the frame blocks (-1: none)
+  const int c_last = (c0 + kMts1Cols - 1 < frame_end ? c0 + kMts1Cols - 1 : frame_end - 1);
+  const int cf_lo = c0 < frame_end ? c0 / p.bpf : -1;
+  const int cf_hi = c0 < frame_end ? c_last / p.bpf : -1;
+  double cacc[kMts1Cols];
 #pragma unroll
-    for (int j = 0; j < kMts1Cols; ++j) {
-      cacc[j] = 0.0;
-      cframe[j] = c0 + j < frame_end ? (c0 + j) / p.bpf : -1;
-    }
-    for (int s0 = 0; s0 < rows; s0 += kMts1Sub) {
+  for (int j = 0; j < kMts1Cols; ++j) cacc[j] = 0.0;
+  double fsum = 0.0;
+  if (c0 < n) {
+    for (int s0 = 0; s0 < kMts1Slab; s0 += kMts1Sub) {
+      if (rs + s0 >= n) break;
       double dacc[kMts1Diag];
 #pragma unroll
       for (int d = 0; d < kMts1Diag; ++d) dacc[d] = 0.0;
-      if (c0 < n) {
 #pragma unroll
-        for (int rr = 0; rr < kMts1Sub; ++rr) {
-          const int rl = s0 + rr;  // row within the block
-          if (rl < rows) {
-            const uint16_t* row = base + static_cast<int64_t>(rl) * n;
-            uint16_t v[kMts1Cols];
-            if constexpr (kVec) {
-              const u32x4 w = *reinterpret_cast<const u32x4*>(row + c0);
+      for (int rr = 0; rr < kMts1Sub; ++rr) {
+        const int r = rs + s0 + rr;
+        if (r < n) {
+          const uint16_t* row = base + static_cast<int64_t>(r) * n;
+          uint16_t v[kMts1Cols];
+          if constexpr (kVec) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(row + c0);
 #pragma unroll
-              for (int j = 0; j < kMts1Cols; ++j) v[j] = u16_at(w, j);
-            } else {
+            for (int j = 0; j < kMts1Cols; ++j) v[j] = u16_at(w, j);
+          } else {
 #pragma unroll
-              for (int j = 0; j < kMts1Cols; ++j) v[j] = c0 + j < n ? row[c0 + j] : 0;
-            }
-            const int r = r0 + rl;
-            const int rframe = r < frame_end ? r / p.bpf : -2;
-            double fr = 0.0;
+            for (int j = 0; j < kMts1Cols; ++j) v[j] = c0 + j < n ? row[c0 + j] : 0;
+          }
+          double x[kMts1Cols];
 #pragma unroll
-            for (int j = 0; j < kMts1Cols; ++j) {
-              const double x = static_cast<double>(Fp16::to_float(v[j]));
-              cacc[j] += x;
-              dacc[j - rr + kMts1Sub - 1] += x;
-              if (cframe[j] == rframe) fr += x;
-            }
-            fsum += fr;
+          for (int j = 0; j < kMts1Cols; ++j) {
+            x[j] = static_cast<double>(Fp16::to_float(v[j]));
+            cacc[j] += x[j];
+            dacc[j - rr + kMts1Sub - 1] += x[j];
+          }
+          // frame-block cells: only rows whose frame meets the owned columns
+          const int rframe = r < frame_end ? r / p.bpf : -2;
+          if (rframe >= cf_lo && rframe <= cf_hi) {
+#pragma unroll
+            for (int j = 0; j < kMts1Cols; ++j)
+              if (c0 + j < frame_end && (c0 + j) / p.bpf == rframe) fsum += x[j];
           }
         }
-        // local diagonal of accumulator d: kl = c0 + d - 15 - s0 + 63
+      }
+      // local diagonal kl = (c - C0) - (r - R0) + 511 of accumulator d
 #pragma unroll
-        for (int d = 0; d < kMts1Diag; ++d) {
-          const int kl = c0 + d - (kMts1Sub - 1) - s0 + (kMts1Rows - 1);
-          if (dacc[d] != 0.0 && kl >= 0 && kl < ndl) atomicAdd(&mts1_diag[kl], dacc[d]);
-        }
+      for (int d = 0; d < kMts1Diag; ++d) {
+        const int kl = (c0 - C0) + d - (kMts1Sub - 1) - (rs - R0) - s0 + (kMts1TileR - 1);
+        if (dacc[d] != 0.0) atomicAdd(&s_diag[kl], dacc[d]);
       }
     }
-    if (c0 < n) {
-#pragma unroll
-      for (int j = 0; j < kMts1Cols; ++j)
-        if (c0 + j < n) mts1_flush(p, out0 + nd + c0 + j, cacc[j]);
-    }
   }
-  // frame-block partial of the workgroup: each thread's sum (at most 32 x 64 cells) is
-  // exact in fp64 and converts exactly to int64 units; the workgroup adds them as integers
+#pragma unroll
+  for (int j = 0; j < kMts1Cols; ++j) s_col[tr][tc * kMts1Cols + j] = cacc[j];
+  // frame-block partial of the workgroup: each thread's sum (at most 512 cells) is exact in
+  // fp64 and converts exactly to int64 units; the workgroup adds them as integers
   long long fq = 0;
   if (__builtin_isfinite(fsum))
     fq = static_cast<long long>(fsum * 0x1p24);
@@ -256,14 +269,21 @@ __global__ __launch_bounds__(kMts1Threads) void mts1_kernel(Mts1Params p) {
   if ((tid & 63) == 0) s_frame[tid >> 6] = fq;
   __syncthreads();
   if (tid == 0) {
-    long long t = 0;
-    for (int w = 0; w < kMts1Threads / 64; ++w) t += s_frame[w];
-    if (t != 0) atomicAdd(&p.acc[out0 + F - 1], static_cast<unsigned long long>(t));
+    long long tot = 0;
+    for (int w = 0; w < kMts1Threads / 64; ++w) tot += s_frame[w];
+    if (tot != 0) atomicAdd(&p.acc[out0 + F - 1], static_cast<unsigned long long>(tot));
   }
-  // diagonal partials: global index k = kl + n - 64 - r0
-  for (int kl = tid; kl < ndl; kl += kMts1Threads) {
-    const int k = kl + n - kMts1Rows - r0;
-    if (k >= 0 && k < nd) mts1_flush(p, out0 + k, mts1_diag[kl]);
+  // column partials: the eight slabs' sums of one column (at most 512 cells, exact)
+  for (int c = tid; c < kMts1TileC; c += kMts1Threads) {
+    double sum = 0.0;
+#pragma unroll
+    for (int sl = 0; sl < kMts1Slabs; ++sl) sum += s_col[sl][c];
+    if (C0 + c < n) mts1_flush(p, out0 + nd + C0 + c, sum);
+  }
+  // diagonal partials: global index k = (c - r) + n - 1 = kl - 511 + C0 - R0 + n - 1
+  for (int kl = tid; kl < kMts1TileDiag; kl += kMts1Threads) {
+    const int k = kl - (kMts1TileR - 1) + C0 - R0 + n - 1;
+    if (k >= 0 && k < nd) mts1_flush(p, out0 + k, s_diag[kl]);
   }
 }
 
@@ -682,27 +702,21 @@ extern "C" int moddit_mts(const void* map, int map_dtype, int heads, int n, int 
     q.heads = heads;
     q.n = n;
     q.bpf = blocks_per_frame;
-    q.n_rblk = (n + kMts1Rows - 1) / kMts1Rows;
+    q.n_rt = (n + kMts1TileR - 1) / kMts1TileR;
+    q.n_ct = (n + kMts1TileC - 1) / kMts1TileC;
     const int64_t total = static_cast<int64_t>(heads) * 3 * n;
     q.acc = static_cast<unsigned long long*>(workspace);
     q.special = reinterpret_cast<float*>(q.acc + total);
     q.out = mts_out;
-    const int64_t grid = static_cast<int64_t>(heads) * q.n_rblk;
+    const int64_t grid = static_cast<int64_t>(heads) * q.n_rt * q.n_ct;
     MODDIT_CHECK_ARG(grid < 0x7fffffff, "mts: shape too large");
     int64_t fill = (total + 255) / 256;
     if (fill > 4096) fill = 4096;
     hipLaunchKernelGGL(mts1_zero_kernel, dim3(static_cast<unsigned>(fill)), dim3(256), 0, st, q);
     MODDIT_CHECK_LAUNCH("mts (zero)");
-    const size_t lds = static_cast<size_t>(n + kMts1Rows - 1) * sizeof(double);
-    static LaunchSetup once_vec, once_scalar;
     const bool vec = n % 8 == 0 && aligned16(map);
     auto kernel = vec ? mts1_kernel<true> : mts1_kernel<false>;
-    if (set_dynamic_lds_once(vec ? once_vec : once_scalar, reinterpret_cast<const void*>(kernel),
-                             (kMts1MaxN + kMts1Rows - 1) * 8) != hipSuccess) {
-      set_error("mts: cannot reserve LDS");
-      return MODDIT_EHIP;
-    }
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(kMts1Threads), lds, st, q);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(kMts1Threads), 0, st, q);
     MODDIT_CHECK_LAUNCH("mts");
     hipLaunchKernelGGL(mts1_finalize_kernel, dim3(static_cast<unsigned>(fill)), dim3(256), 0, st, q);
     MODDIT_CHECK_LAUNCH("mts (finalize)");

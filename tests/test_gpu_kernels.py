@@ -424,8 +424,9 @@ def test_mts_bit_exact_on_map_domain(n, bpf):
 @pytest.mark.parametrize("n,bpf,H", [(37, 5, 2), (120, 9, 2), (2112, 64, 1)])
 def test_mts_arbitrary_fp16_inputs(n, bpf, H):
     """Any finite fp16 (both signs, subnormals, up to 65504): exact sums rounded once.
-    n=37: the scalar-load path; n=120: 16-byte loads; n=2112: two column chunks per
-    workgroup (each thread owns 8 columns of 2048 per chunk)."""
+    n=37: the scalar-load path; n=120: 16-byte loads; n=2112: 5 x 9 tiles of 512 rows x
+    256 columns per head, the last row and column tiles partial (64 of 512 rows, 64 of 256
+    columns)."""
     rng = np.random.default_rng(n)
     bits = rng.integers(0, 0x7C00, size=(H, n, n)).astype(np.uint16)
     bits |= (rng.integers(0, 2, size=bits.shape) << 15).astype(np.uint16)
