@@ -492,18 +492,31 @@ struct MaskParams {
   int kv_tiles;            // key tiles at or beyond are dropped (from_mask only)
 };
 
+// LDS of the line-based mask kernel: column bytes, then the diagonal bytes at an 8-byte
+// aligned offset plus 8 bytes of zero padding for the unaligned 8-byte windows.
+__host__ __device__ inline int mask_diag_offset(int n) { return (n + 7) & ~7; }
+__host__ __device__ inline int mask_lds_bytes(int n) {
+  return mask_diag_offset(n) + ((2 * n - 1 + 7) & ~7) + 8;
+}
+
 // Tiles per workgroup: the selected-line byte maps are built in LDS once per workgroup
 // and serve this many consecutive query tiles of the head.
 constexpr int kMaskTilesPerWg = 8;
+static_assert(kMaskTilesPerWg % 4 == 0, "the batched path packs four tiles per 64-bit word");
 constexpr int kMaskCols = 8;  // mask columns per thread and pass
+static_assert(kMaskThreads * kMaskCols * 2 < 65536, "a tile's entry count fits 16 bits");
 
 template <bool kFromMask>
 __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) {
   extern __shared__ __align__(16) unsigned char mk_smem[];
-  uint8_t* colsel = mk_smem;          // n bytes
-  uint8_t* diagsel = mk_smem + p.n;   // 2n-1 bytes
+  // colsel: n bytes; diagsel: 2n-1 bytes at an 8-byte aligned offset, followed by zero
+  // padding so that the 8-byte windows read below stay inside the allocation
+  const int diag_off = mask_diag_offset(p.n);
+  uint8_t* colsel = mk_smem;
+  uint8_t* diagsel = mk_smem + diag_off;
   __shared__ int s_wave[8];
   __shared__ int s_total;
+  __shared__ int s_wpack[kMaskThreads / 64][kMaskTilesPerWg / 2];
 
   const int tid = threadIdx.x;
   const int wg_per_head = (p.n_qtiles + kMaskTilesPerWg - 1) / kMaskTilesPerWg;
@@ -516,7 +529,8 @@ __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) 
 
   if (!kFromMask) {
     mode = p.mode ? p.mode[h] : MODDIT_MODE_SPARSE;
-    for (int i = tid; i < 3 * n - 1; i += kMaskThreads) mk_smem[i] = 0;
+    for (int i = tid; i < mask_lds_bytes(n) / 8; i += kMaskThreads)
+      reinterpret_cast<uint64_t*>(mk_smem)[i] = 0;
     __syncthreads();
     const int32_t* s = p.sel + static_cast<int64_t>(h) * p.k;
     for (int i = tid; i < p.k; i += kMaskThreads) {
@@ -544,6 +558,176 @@ __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) 
   const bool vec_mask = (nb % kMaskCols) == 0 && p.mask_out != nullptr &&
                         (reinterpret_cast<uintptr_t>(p.mask_out) & 7) == 0;
 
+  // Per-column values do not depend on the query tile: computed once per workgroup for
+  // this thread's columns of the first pass (the only pass while nb <= 2048), and on the
+  // fly for the columns of later passes.
+  // Rows are evaluated as 8 bytes (0/1), one per owned column: the selected-column and
+  // text-column bytes are fixed per workgroup, and when the 8 columns are consecutive video
+  // blocks their diagonal bytes for video row iv are the 8 consecutive diagsel bytes from
+  // jv0 - iv + n - 1, read as one unaligned window.
+  int jv_h[kMaskCols], jf_h[kMaskCols];
+  uint64_t col_bytes = 0, text_bytes = 0, valid_bytes = 0;
+  bool all_video = !kFromMask && tid * kMaskCols + kMaskCols <= nb;
+  if (!kFromMask) {
+#pragma unroll
+    for (int c = 0; c < kMaskCols; ++c) {
+      const int j = tid * kMaskCols + c;
+      const int jv = j < nb ? video_index(j) : -1;
+      jv_h[c] = jv;
+      jf_h[c] = (bd && jv >= 0) ? jv / p.bpf : -3;
+      if (j < nb) valid_bytes |= 1ull << (8 * c);
+      if (j < nb && jv < 0) text_bytes |= 1ull << (8 * c);
+      if (jv >= 0 && colsel[jv]) col_bytes |= 1ull << (8 * c);
+      if (jv < 0 || jv != jv_h[0] + c) all_video = false;
+    }
+  }
+  auto row_bytes = [&](bool has, int iv, int ifr) -> uint64_t {
+    if (!has) return 0;
+    if (iv < 0 || full) return valid_bytes;
+    uint64_t r = col_bytes | text_bytes;
+    if (all_video) {
+      const int d0 = jv_h[0] - iv + n - 1;  // in [0, 2n-9]
+      const uint64_t* w = reinterpret_cast<const uint64_t*>(diagsel) + (d0 >> 3);
+      const int sh = (d0 & 7) * 8;
+      const uint64_t lo = w[0];
+      r |= sh ? (lo >> sh) | (w[1] << (64 - sh)) : lo;
+    } else {
+#pragma unroll
+      for (int c = 0; c < kMaskCols; ++c)
+        if (jv_h[c] >= 0 && diagsel[jv_h[c] - iv + n - 1]) r |= 1ull << (8 * c);
+    }
+    if (bd) {
+#pragma unroll
+      for (int c = 0; c < kMaskCols; ++c)
+        if (jf_h[c] == ifr) r |= 1ull << (8 * c);
+    }
+    return r & valid_bytes;
+  };
+  // bit c of the result = byte c (0 or 1) of v; no partial product carries into the top byte
+  auto byte_bits = [](uint64_t v) -> unsigned {
+    return static_cast<unsigned>((v * 0x0102040810204080ull) >> 56);
+  };
+
+  if (!kFromMask && nb <= kMaskThreads * kMaskCols) {
+    // One pass covers every column: evaluate all of the workgroup's tiles first, then place
+    // all of their entries with one scan of the per-thread counts. Row bits and counts of
+    // the tiles sit in 16-bit fields of 64-bit registers, four tiles per register (a
+    // workgroup's count per tile is at most 4096), so the loops stay rolled. Entries here never reach kv_tiles
+    // (line-based masks have no key-tile limit).
+    const int j0 = tid * kMaskCols;
+    uint64_t bits_w[kMaskTilesPerWg / 4];  // tile tt: m0 | m1 << 8 at bits 16 * (tt & 3) of word tt >> 2
+    uint64_t cnt_w[kMaskTilesPerWg / 4];   // tile tt: entry count, same place
+#pragma unroll
+    for (int i = 0; i < kMaskTilesPerWg / 4; ++i) bits_w[i] = cnt_w[i] = 0;
+#pragma unroll 1
+    for (int tt = 0; tt < t_end - t_begin; ++tt) {
+      const int t = t_begin + tt;
+      const int r0 = t * rows_per_tile;
+      const int r1 = r0 + 1;
+      const bool has_r0 = r0 < n_rows;
+      const bool has_r1 = rows_per_tile == 2 && r1 < n_rows;
+      const int iv0 = video_index(r0);
+      const int iv1 = video_index(r1);
+      const uint64_t b0 = row_bytes(has_r0, iv0, iv0 >= 0 ? iv0 / p.bpf : -2);
+      const uint64_t b1 = row_bytes(has_r1, iv1, iv1 >= 0 ? iv1 / p.bpf : -2);
+      const unsigned m0 = byte_bits(b0);
+      const unsigned m1 = byte_bits(b1);
+      if (p.mask_out && j0 < nb) {
+        uint8_t* row0 = p.mask_out + (static_cast<int64_t>(h) * nb + r0) * nb + j0;
+        if (vec_mask) {
+          if (has_r0) *reinterpret_cast<uint64_t*>(row0) = b0;
+          if (has_r1) *reinterpret_cast<uint64_t*>(row0 + nb) = b1;
+        } else {
+          for (int c = 0; c < kMaskCols && j0 + c < nb; ++c) {
+            if (has_r0) row0[c] = (m0 >> c) & 1;
+            if (has_r1) row0[nb + c] = (m1 >> c) & 1;
+          }
+        }
+      }
+      const int sh = 16 * (tt & 3);
+      const uint64_t cnt = static_cast<uint64_t>(__builtin_popcount(m0 | m1) * tiles_per_col);
+#pragma unroll
+      for (int i = 0; i < kMaskTilesPerWg / 4; ++i) {
+        if (i == (tt >> 2)) {
+          bits_w[i] |= static_cast<uint64_t>(m0 | (m1 << 8)) << sh;
+          cnt_w[i] |= cnt << sh;
+        }
+      }
+    }
+    if (p.counts == nullptr) return;
+    // inclusive scan of the packed counts (four 32-bit words) within the wave, then across
+    // the four waves
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    constexpr int kWords = kMaskTilesPerWg / 2;
+    int own[kWords], incl[kWords];
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) {
+      own[i] = static_cast<int>(cnt_w[i >> 1] >> (32 * (i & 1)));
+      incl[i] = own[i];
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) {
+        const int v = __shfl_up(incl[i], o);
+        if (lane >= o) incl[i] += v;
+      }
+    }
+    if (lane == 63) {
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) s_wpack[wave][i] = incl[i];
+    }
+    __syncthreads();
+    int start[kWords], total[kWords];
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) {
+      int before = 0, all = 0;
+      for (int w = 0; w < kMaskThreads / 64; ++w) {
+        const int v = s_wpack[w][i];
+        if (w < wave) before += v;
+        all += v;
+      }
+      start[i] = before + incl[i] - own[i];
+      total[i] = all;
+    }
+    const bool both = p.block == 128 || p.union_rows;
+#pragma unroll 1
+    for (int tt = 0; tt < t_end - t_begin; ++tt) {
+      const int sh = 16 * (tt & 1);
+      int st = 0, tl = 0;
+#pragma unroll
+      for (int i = 0; i < kWords; ++i)
+        if (i == (tt >> 1)) {
+          st = start[i];
+          tl = total[i];
+        }
+      int pos = (st >> sh) & 0xffff;
+      const int tot = (tl >> sh) & 0xffff;
+      const int64_t slot = static_cast<int64_t>(h) * p.n_qtiles + t_begin + tt;
+      int32_t* out = p.entries + slot * p.cap;
+      uint64_t bw = 0;
+#pragma unroll
+      for (int i = 0; i < kMaskTilesPerWg / 4; ++i)
+        if (i == (tt >> 2)) bw = bits_w[i];
+      const unsigned rb = static_cast<unsigned>(bw >> (16 * (tt & 3))) & 0xffffu;
+      const unsigned m0 = rb & 0xffu;
+      const unsigned m1 = rb >> 8;
+      unsigned rem = m0 | m1;
+      while (rem != 0u) {
+        const int c = __builtin_ctz(rem);
+        rem &= rem - 1u;
+        const int rbits = both ? 3 : static_cast<int>((m0 >> c) & 1u) | (static_cast<int>((m1 >> c) & 1u) << 1);
+        for (int s2 = 0; s2 < tiles_per_col; ++s2) {
+          if (pos < p.cap) out[pos] = ((((j0 + c) * tiles_per_col + s2)) << 2) | rbits;
+          ++pos;
+        }
+      }
+      if (tid == 0) p.counts[slot] = tot < p.cap ? tot : p.cap;
+    }
+    return;
+  }
+
   for (int t = t_begin; t < t_end; ++t) {
     const int r0 = t * rows_per_tile;
     const int r1 = r0 + 1;
@@ -559,8 +743,16 @@ __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) 
     for (int jb = 0; jb < nb; jb += kMaskThreads * kMaskCols) {
       const int j0 = jb + tid * kMaskCols;
       unsigned m0 = 0, m1 = 0;  // bit c: column j0 + c is active in row r0 / r1
+      uint64_t b0 = 0, b1 = 0;  // byte c: the same as 0/1 (mask output)
+      const bool fast = !kFromMask && jb == 0;
+      if (fast) {
+        b0 = row_bytes(has_r0, iv0, if0);
+        b1 = row_bytes(has_r1, iv1, if1);
+        m0 = byte_bits(b0);
+        m1 = byte_bits(b1);
+      }
 #pragma unroll
-      for (int c = 0; c < kMaskCols; ++c) {
+      for (int c = 0; c < kMaskCols && !fast; ++c) {
         const int j = j0 + c;
         if (j >= nb) break;
         bool a0, a1;
@@ -569,8 +761,9 @@ __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) 
           a0 = has_r0 && col[r0 * p.in_row_stride] != 0;
           a1 = has_r1 && col[r1 * p.in_row_stride] != 0;
         } else {
+          // columns of later passes (nb > 2048)
           const int jv = video_index(j);
-          const int jf = jv >= 0 ? jv / p.bpf : -3;
+          const int jf = (bd && jv >= 0) ? jv / p.bpf : -3;
           const bool colj = jv >= 0 && colsel[jv];
           a0 = has_r0 && (iv0 < 0 || jv < 0 || full || colj || diagsel[jv - iv0 + n - 1] ||
                           (bd && if0 == jf));
@@ -582,13 +775,14 @@ __global__ __launch_bounds__(kMaskThreads) void mask_tiles_kernel(MaskParams p) 
       }
       if (!kFromMask && p.mask_out && j0 < nb) {
         uint8_t* row0 = p.mask_out + (static_cast<int64_t>(h) * nb + r0) * nb + j0;
-        if (vec_mask) {
-          uint64_t b0 = 0, b1 = 0;  // bit c -> byte c (0/1)
+        if (!fast) {
 #pragma unroll
           for (int c = 0; c < kMaskCols; ++c) {
             b0 |= static_cast<uint64_t>((m0 >> c) & 1u) << (8 * c);
             b1 |= static_cast<uint64_t>((m1 >> c) & 1u) << (8 * c);
           }
+        }
+        if (vec_mask) {
           if (has_r0) *reinterpret_cast<uint64_t*>(row0) = b0;
           if (has_r1) *reinterpret_cast<uint64_t*>(row0 + nb) = b1;
         } else {
@@ -866,7 +1060,7 @@ extern "C" int moddit_mask_from_lines(const int32_t* sel, int heads, int k, cons
   p.n_qtiles = n_qtiles;
   p.cap = cap;
   p.kv_tiles = 0x7fffffff;
-  const size_t lds = static_cast<size_t>(3 * n);
+  const size_t lds = static_cast<size_t>(mask_lds_bytes(n));
   MODDIT_CHECK_ARG(lds <= 65536, "mask_from_lines: n=%d too large", n);
   const int64_t grid = static_cast<int64_t>(heads) * ((n_qtiles + kMaskTilesPerWg - 1) / kMaskTilesPerWg);
   hipLaunchKernelGGL(mask_tiles_kernel<false>, dim3(static_cast<unsigned>(grid)),

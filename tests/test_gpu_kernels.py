@@ -534,9 +534,13 @@ def test_check_bd():
 @pytest.mark.parametrize("model_type", ["wan", "hunyuan", "cogvideox", "other"])
 @pytest.mark.parametrize("bs", [64, 128])
 @pytest.mark.parametrize("union", [False, True])
-def test_mask_from_lines_bit_exact(model_type, bs, union):
-    rng = np.random.default_rng(hash((model_type, bs, union)) % 2**32)
-    H, n, bpf, k = 5, 23, 4, 7
+@pytest.mark.parametrize("n,bpf,k", [(23, 4, 7), (301, 12, 60)])
+def test_mask_from_lines_bit_exact(model_type, bs, union, n, bpf, k):
+    """n=301: most threads own 8 consecutive video columns and read their diagonal bytes
+    as one 8-byte window, at every alignment; threads at the text boundary and the last,
+    partial thread take the per-column path."""
+    rng = np.random.default_rng(hash((model_type, bs, union, n)) % 2**32)
+    H = 5
     tb = 3 if model_type in ("hunyuan", "cogvideox") else 0
     nb = n + tb
     sel = rng.integers(0, 3 * n - 1, size=(H, k)).astype(np.int32)
