@@ -139,7 +139,13 @@ __global__ __launch_bounds__(kGemvThreads) void fit_gemv_kernel(const double* __
                                                                 const double* __restrict__ y,
                                                                 double* __restrict__ xcb,
                                                                 int heads, int m) {
-  __shared__ double s_y[kGemvHeads][kGemvChunk];
+  // y chunks are double-buffered in LDS; the next chunk's y values and this lane's S^-1
+  // elements of it are loaded before the current chunk's products, so one barrier per
+  // chunk separates the products from the next chunk's LDS writes
+  __shared__ double s_y[2][kGemvHeads][kGemvChunk];
+  constexpr int kPer = kGemvChunk / kGemvLanes;                 // S^-1 elements per lane
+  constexpr int kStage = kGemvHeads * kGemvChunk / kGemvThreads;  // y values per thread
+  static_assert(kGemvHeads * kGemvChunk % kGemvThreads == 0, "y chunk staging");
   const int tid = threadIdx.x;
   const int r = tid / kGemvLanes;
   const int j = tid % kGemvLanes;
@@ -150,21 +156,55 @@ __global__ __launch_bounds__(kGemvThreads) void fit_gemv_kernel(const double* __
 #pragma unroll
   for (int hh = 0; hh < kGemvHeads; ++hh) acc[hh] = 0.0;
   const double* srow = sinv + static_cast<int64_t>(row < m ? row : m - 1) * m;
-  for (int k0 = 0; k0 < m; k0 += kGemvChunk) {
-    for (int i = tid; i < kGemvHeads * kGemvChunk; i += kGemvThreads) {
+  auto load_y = [&](int k0, double* v) {
+#pragma unroll
+    for (int q = 0; q < kStage; ++q) {
+      const int i = tid + q * kGemvThreads;
       const int hh = i / kGemvChunk;
       const int g = k0 + i % kGemvChunk;
-      s_y[hh][i % kGemvChunk] = (hh < nh && g < m) ? y[static_cast<int64_t>(h0 + hh) * m + g] : 0.0;
+      v[q] = (hh < nh && g < m) ? y[static_cast<int64_t>(h0 + hh) * m + g] : 0.0;
     }
-    __syncthreads();
+  };
+  auto store_y = [&](int buf, const double* v) {
 #pragma unroll
-    for (int t = 0; t < kGemvChunk / kGemvLanes; ++t) {
+    for (int q = 0; q < kStage; ++q) {
+      const int i = tid + q * kGemvThreads;
+      s_y[buf][i / kGemvChunk][i % kGemvChunk] = v[q];
+    }
+  };
+  auto load_a = [&](int k0, double* a) {
+#pragma unroll
+    for (int t = 0; t < kPer; ++t) {
       const int g = k0 + j + kGemvLanes * t;
-      const double a = g < m ? srow[g] : 0.0;
+      a[t] = g < m ? srow[g] : 0.0;
+    }
+  };
+  double a_cur[kPer], yv[kStage];
+  load_y(0, yv);
+  load_a(0, a_cur);
+  store_y(0, yv);
+  __syncthreads();
+  int buf = 0;
+  for (int k0 = 0; k0 < m; k0 += kGemvChunk) {
+    const bool more = k0 + kGemvChunk < m;
+    double a_nxt[kPer];
+    if (more) {
+      load_y(k0 + kGemvChunk, yv);
+      load_a(k0 + kGemvChunk, a_nxt);
+    }
 #pragma unroll
-      for (int hh = 0; hh < kGemvHeads; ++hh) acc[hh] = __builtin_fma(a, s_y[hh][j + kGemvLanes * t], acc[hh]);
+    for (int t = 0; t < kPer; ++t) {
+#pragma unroll
+      for (int hh = 0; hh < kGemvHeads; ++hh)
+        acc[hh] = __builtin_fma(a_cur[t], s_y[buf][hh][j + kGemvLanes * t], acc[hh]);
+    }
+    if (more) {
+      store_y(buf ^ 1, yv);
+#pragma unroll
+      for (int t = 0; t < kPer; ++t) a_cur[t] = a_nxt[t];
     }
     __syncthreads();
+    buf ^= 1;
   }
 #pragma unroll
   for (int hh = 0; hh < kGemvHeads; ++hh) {
