@@ -126,6 +126,11 @@ def test_c_abi_rejects_bad_arguments_before_any_launch():
     rc = lib.moddit_block_sparse_fwd_q8(P, P, P, P, P, P, P, P, P, 1, 1, 300, 300, 64, s, 0.1, 0,
                                         P, P, 1, 1, 0, None)
     assert rc == _lib.MODDIT_EINVAL and b"needs 3" in lib.moddit_last_error()
+    # fp16 M^T S: n beyond the int64 accumulators' range, unaligned workspace
+    rc = lib.moddit_mts(P, _lib.FP16, 1, (1 << 20) + 1, 4, P, P, None)
+    assert rc == _lib.MODDIT_EINVAL and b"exceeds" in lib.moddit_last_error()
+    rc = lib.moddit_mts(P, _lib.FP16, 1, 64, 4, P + 8, P, None)
+    assert rc == _lib.MODDIT_EINVAL and b"aligned" in lib.moddit_last_error()
     with pytest.raises(_lib.ModditError, match="mtm"):
         _lib.check(lib.moddit_mtm_host(-1, 1, 1.0, None), "moddit_mtm_host")
 
