@@ -126,11 +126,12 @@ __global__ __launch_bounds__(kFitThreads) void fit_rhs_kernel(const float* __res
   if (threadIdx.x == 0) yh[n] = static_cast<double>(m[F - 1]) - wb;
 }
 
-// x_cb[h] = S^-1 y[h] for all heads. Workgroup = 16 rows of S^-1 x up to 16 heads; 16
+// x_cb[h] = S^-1 y[h] for all heads. Workgroup = 8 rows of S^-1 x up to 16 heads; 32
 // threads per row stride the reduction, and y chunks are staged in LDS and shared by the
-// rows (measured at n = 1800, H = 24: the fastest of the row x head blockings tried).
+// rows (measured at n = 1800 and 1080, H = 24 and 40: the fastest of the row x head
+// blockings tried, 4 to 32 rows and 16 or 24 heads).
 constexpr int kGemvThreads = 256;
-constexpr int kGemvRows = 16;
+constexpr int kGemvRows = 8;
 constexpr int kGemvLanes = kGemvThreads / kGemvRows;  // threads per row
 constexpr int kGemvHeads = 16;
 constexpr int kGemvChunk = 128;
