@@ -25,7 +25,9 @@ import json
 import math
 import os
 import platform
+import statistics
 import sys
+import threading
 import time
 
 import torch
@@ -157,7 +159,7 @@ def measured_traffic(name="attention_hunyuan_headline.md"):
     return None, None
 
 
-def mfma_ceiling(kind, iters=4000, reps=3, zeros=False):
+def mfma_ceiling(kind, iters=4000, reps=200, zeros=False):
     """MFMA rate and shader clock on random operands, from the calibration library built
     next to libmoddit.so (mod-dit_amd/csrc/calib/mfma_ceiling.hip): back-to-back MFMAs
     only, two waves per SIMD, one 8-wave workgroup per CU. kind 0: bf16 32x32x16, 1: int8
@@ -181,6 +183,91 @@ def mfma_ceiling(kind, iters=4000, reps=3, zeros=False):
     return {"value": round(rate.value, 1), "unit": "TOP/s" if kind == 1 else "TFLOP/s",
             "clock_mhz": round(mhz.value), "cycles_per_mfma_per_simd": round(cyc.value, 2),
             "mfma": names[kind], "operands": "zeros" if zeros else "random"}
+
+
+class BoardSampler:
+    """Board power and graphics clock over a timed region, sampled every 50 ms on a
+    background thread with read-only amdsmi metric queries (current_socket_power,
+    current_gfxclk; the power cap from amdsmi_get_power_cap_info). Under sustained MFMA
+    load on real data the board sits at its power limit and the clock falls below its
+    2.4 GHz maximum; these figures show where a run stands. `result()` is None when amdsmi
+    is missing or its queries fail."""
+
+    def __init__(self, period_s: float = 0.05, skip_s: float = 1.0):
+        # the firmware refreshes these metrics with some lag: samples from the first
+        # `skip_s` seconds of a region still show the load before it and are dropped
+        self.period_s = period_s
+        self.skip_s = skip_s
+        self.samples: list[tuple[float, float, float]] = []
+        self.cap_w = None
+        self._smi = None
+
+    def __enter__(self):
+        try:
+            import amdsmi  # noqa: PLC0415
+
+            amdsmi.amdsmi_init()
+            self._h = amdsmi.amdsmi_get_processor_handles()[0]
+            cap = amdsmi.amdsmi_get_power_cap_info(self._h).get("power_cap")
+            self.cap_w = round(cap / 1e6, 1) if isinstance(cap, (int, float)) and cap > 0 else None
+            self._smi = amdsmi
+        except Exception:  # noqa: BLE001 - telemetry is optional
+            self._smi = None
+            return self
+        self._t0 = time.perf_counter()
+        self._stop = threading.Event()
+        self._thread = threading.Thread(target=self._run, daemon=True)
+        self._thread.start()
+        return self
+
+    def _run(self):
+        while not self._stop.is_set():
+            try:
+                m = self._smi.amdsmi_get_gpu_metrics_info(self._h)
+                pw, clk = m.get("current_socket_power"), m.get("current_gfxclk")
+                # the metrics table marks missing fields with 0xFFFF / 0xFFFFFFFF
+                if all(isinstance(x, (int, float)) and 0 < x < 60000 for x in (pw, clk)):
+                    self.samples.append((time.perf_counter() - self._t0, float(pw), float(clk)))
+            except Exception:  # noqa: BLE001
+                pass
+            self._stop.wait(self.period_s)
+
+    def __exit__(self, *exc):
+        if self._smi is not None:
+            self._stop.set()
+            self._thread.join()
+            try:
+                self._smi.amdsmi_shut_down()
+            except Exception:  # noqa: BLE001
+                pass
+        return False
+
+    def result(self):
+        kept = [x for x in self.samples if x[0] >= self.skip_s]
+        if not kept:
+            return None
+        pw = [x[1] for x in kept]
+        clk = [x[2] for x in kept]
+        return {"power_w": round(statistics.mean(pw), 1), "power_w_max": max(pw),
+                "power_cap_w": self.cap_w, "gfxclk_mhz": round(statistics.mean(clk)),
+                "gfxclk_mhz_max_of_part": 2400, "samples": len(pw),
+                "source": f"amdsmi gpu_metrics current_socket_power / current_gfxclk every "
+                          f"{int(self.period_s * 1e3)} ms, first {self.skip_s:g} s dropped"}
+
+
+def sampled_loop(fn, seconds=4.0):
+    """Calls fn until `seconds` have passed (synchronising every call) under a
+    BoardSampler; returns (ms per call, board figures)."""
+    fn()
+    torch.cuda.synchronize()
+    with BoardSampler() as board:
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            fn()
+            torch.cuda.synchronize()
+            n += 1
+        wall = time.perf_counter() - t0
+    return wall * 1e3 / n, board.result()
 
 
 def time_events(fn, reps):
@@ -601,10 +688,30 @@ def main(argv=None):
         return 2
 
     if args.calibrate:
-        rows = [mfma_ceiling(kind, zeros=z) for kind in (0, 1, 2) for z in (False, True)]
+        rows = []
+        for kind in (0, 1, 2):
+            for z in (False, True):
+                # one call of ~800 back-to-back launches (~4 s): no gaps under the sampler
+                with BoardSampler() as board:
+                    row = mfma_ceiling(kind, reps=800 if kind != 2 else 400, zeros=z)
+                if row is not None:
+                    row["board"] = board.result()
+                rows.append(row)
+        # the same dense attention kernel on the headline layer's data and on all-zero
+        # inputs: the cycle count barely changes, the clock does (power limit)
+        c = CONFIGS["hunyuan"]
+        q, k, v = synth_qkv(c["H"], c["F"], c["Hp"], c["Wp"], c["D"], seed=0)
+        o = torch.empty_like(q)
+        z = torch.zeros_like(q)
+        attn = {}
+        for name, args_ in (("headline data", (q, k, v)), ("all-zero inputs", (z, z, z))):
+            ms, board = sampled_loop(lambda a=args_: ops.flash_fwd(*a, return_lse=False, out=o), 5.0)
+            attn[name] = {"ms_per_call": round(ms, 3), "board": board,
+                          "mcycles": (round(ms * board["gfxclk_mhz"] / 1e3, 1) if board else None)}
         print(json.dumps({"metric": "MFMA ceiling by operand data", "published_peak": {
             "bf16": MI355X_BF16_DENSE_TFLOPS, "int8": INT8_FP8_PEAK_TFLOPS,
-            "fp8": INT8_FP8_PEAK_TFLOPS}, "rows": rows}), flush=True)
+            "fp8": INT8_FP8_PEAK_TFLOPS}, "rows": rows,
+            "dense_attention_hunyuan_layer": attn}), flush=True)
         return 0 if all(rows) else 1
 
     if args.profile == "copy":
@@ -696,6 +803,15 @@ def main(argv=None):
     dense_ms_list = time_events(lambda: ops.flash_fwd(q, k, v, return_lse=False, out=dense_out),
                                 args.dense_reps)
     dense_ms = sorted(dense_ms_list)[len(dense_ms_list) // 2]
+
+    log("board power and clock under the sparse and the dense call (4 s each)")
+    board_ms, board = sampled_loop(sparse_call)
+    if board is not None:
+        board["ms_per_call"] = round(board_ms, 3)
+    dense_board_ms, dense_board = sampled_loop(
+        lambda: ops.flash_fwd(q, k, v, return_lse=False, out=dense_out))
+    if dense_board is not None:
+        dense_board["ms_per_call"] = round(dense_board_ms, 3)
 
     log("timing mask-prediction overhead")
     for _ in range(2):
@@ -792,7 +908,9 @@ def main(argv=None):
             "kernel_ms": round(kernel_ms, 4),
             "mfma_ceiling": ceiling,
             "frac_of_mfma_ceiling": (round(achieved / ceiling["value"], 4) if ceiling else None),
+            "board": board,
         },
+        "dense_board": dense_board,
         "cpu_baseline": cpu,
         "q8": q8,
         "host": {"cpu_count": os.cpu_count(), "machine": platform.processor() or platform.machine(),

@@ -146,9 +146,11 @@ extern "C" {
 
 // Runs `reps` timed launches of `iters` loop trips (16 MFMAs per wave per trip) on the
 // current device, one 8-wave workgroup per CU, random operands (or all-zero ones when
-// `zeros` is set), and reports the best rate in TFLOP/s (TOP/s for int8), the mean shader
-// clock in MHz of that launch, and the shader cycles per MFMA per SIMD. Returns 0, or 1
-// on a HIP error (message on stderr), or 2 for a bad argument.
+// `zeros` is set), and reports the sustained rate over those launches in TFLOP/s (TOP/s
+// for int8), their mean shader clock in MHz, and the shader cycles per MFMA per SIMD.
+// The board's power control settles over tens of milliseconds, so a few hundred launches
+// (~1 s) give the rate the part holds under load. Returns 0, or 1 on a HIP error (message
+// on stderr), or 2 for a bad argument.
 int moddit_calib_mfma(int kind, int zeros, int iters, int reps, double* rate, double* clock_mhz,
                       double* cycles_per_mfma) {
   if (kind < 0 || kind > 2 || iters <= 0 || reps <= 0 || rate == nullptr ||
@@ -160,7 +162,8 @@ int moddit_calib_mfma(int kind, int zeros, int iters, int reps, double* rate, do
   unsigned long long* clk = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   std::vector<unsigned long long> host;
-  double best_ms = 1e30, best_mhz = 0.0;
+  double total_ms = 0.0, mhz_sum = 0.0;
+  int mhz_n = 0;
   CALIB_CHECK(hipGetDevice(&dev));
   CALIB_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   CALIB_CHECK(hipMalloc(&out, static_cast<size_t>(cus) * kThreads * sizeof(float)));
@@ -181,8 +184,8 @@ int moddit_calib_mfma(int kind, int zeros, int iters, int reps, double* rate, do
     CALIB_CHECK(hipEventSynchronize(e1));
     float ms = 0.f;
     CALIB_CHECK(hipEventElapsedTime(&ms, e0, e1));
-    if (rep == 0 || ms >= best_ms) continue;
-    best_ms = ms;
+    if (rep == 0) continue;
+    total_ms += ms;
     CALIB_CHECK(hipMemcpy(host.data(), clk, host.size() * sizeof(unsigned long long),
                           hipMemcpyDeviceToHost));
     double sum = 0.0;
@@ -192,13 +195,17 @@ int moddit_calib_mfma(int kind, int zeros, int iters, int reps, double* rate, do
         sum += static_cast<double>(host[2 * w]) / static_cast<double>(host[2 * w + 1]) * 100.0;
         ++n;
       }
-    best_mhz = n > 0 ? sum / n : 0.0;
+    if (n > 0) {
+      mhz_sum += sum / n;
+      ++mhz_n;
+    }
   }
   {
-    const double mfmas = static_cast<double>(cus) * (kThreads / 64) * iters * 16.0;
-    *rate = mfmas * kFlopPerMfma[kind] / (best_ms * 1e-3) / 1e12;
-    *clock_mhz = best_mhz;
-    *cycles_per_mfma = best_ms * 1e-3 * best_mhz * 1e6 / (mfmas / (cus * 4.0));
+    const double mfmas = static_cast<double>(cus) * (kThreads / 64) * iters * 16.0 * reps;
+    const double mhz = mhz_n > 0 ? mhz_sum / mhz_n : 0.0;
+    *rate = mfmas * kFlopPerMfma[kind] / (total_ms * 1e-3) / 1e12;
+    *clock_mhz = mhz;
+    *cycles_per_mfma = total_ms * 1e-3 * mhz * 1e6 / (mfmas / (cus * 4.0));
   }
 done:
   if (e0) (void)hipEventDestroy(e0);
