@@ -631,6 +631,9 @@ def q8_leg(q, k, v, tiles, out, *, ref, eff_flop, exec_flop, reps):
     sp = time_events(lambda: ops.block_sparse_fwd_q8(qz, tiles, out=out), max(3, reps // 2))
     dn = time_events(lambda: ops.flash_fwd_q8(qz, return_lse=False, out=out), 2)
     quant_ms, sparse_ms, dense_ms = min(quant), sum(sp) / len(sp), min(dn)
+    board_ms, board = sampled_loop(lambda: ops.block_sparse_fwd_q8(qz, tiles, out=out))
+    if board is not None:
+        board["ms_per_call"] = round(board_ms, 3)
     return {
         "dtype": "int8 Q.K^T, fp8 e4m3 P.V, fp32 softmax",
         "quantize_ms": round(quant_ms, 3),
@@ -644,6 +647,7 @@ def q8_leg(q, k, v, tiles, out, *, ref, eff_flop, exec_flop, reps):
         "dense_tflops": round(eff_flop / (dense_ms * 1e-3) / 1e12, 3),
         "vs_bf16_sparse_max_abs": round(err_max, 5),
         "vs_bf16_sparse_mean_abs": round(err_mean, 6),
+        "sparse_board": board,
     }
 
 
