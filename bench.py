@@ -39,6 +39,9 @@ import mod_dit_amd as md  # noqa: E402
 from mod_dit_amd import ops  # noqa: E402
 
 MI355X_BF16_DENSE_TFLOPS = 2500.0
+# dense bf16 MFMA FLOP per shader cycle of the whole part: 256 CUs x 4 SIMDs x one
+# 32x32x16 MFMA (32,768 FLOP) per 32 cycles; x 2.384 GHz = the published 2.5 PFLOP/s
+MI355X_BF16_FLOP_PER_CYCLE = 256 * 4 * 1024
 MI355X_HBM_GBPS = 8000.0
 
 CONFIGS = {
@@ -913,8 +916,20 @@ def main(argv=None):
             "mfma_ceiling": ceiling,
             "frac_of_mfma_ceiling": (round(achieved / ceiling["value"], 4) if ceiling else None),
             "board": board,
+            # the same peak at the clock the board held under this call (BASELINE.md's
+            # "fraction of the bf16 MFMA peak computed from the measured clock"); amdsmi's
+            # gfx clock reads ~2.5 % above the shader-cycle clock, so this errs low
+            "peak_at_measured_clock": (round(MI355X_BF16_FLOP_PER_CYCLE * board["gfxclk_mhz"] * 1e6
+                                             / 1e12, 1) if board else None),
+            "frac_at_measured_clock": (round(achieved / (MI355X_BF16_FLOP_PER_CYCLE
+                                                         * board["gfxclk_mhz"] * 1e6 / 1e12), 4)
+                                       if board else None),
         },
         "dense_board": dense_board,
+        "dense_frac_at_measured_clock": (
+            round(eff_flop / (dense_ms * 1e-3) / (MI355X_BF16_FLOP_PER_CYCLE
+                                                  * dense_board["gfxclk_mhz"] * 1e6), 4)
+            if dense_board else None),
         "cpu_baseline": cpu,
         "q8": q8,
         "host": {"cpu_count": os.cpu_count(), "machine": platform.processor() or platform.machine(),
