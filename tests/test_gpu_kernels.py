@@ -75,6 +75,33 @@ def _random_block_mask(H, nb, density, seed, diag=True):
     return m
 
 
+@pytest.mark.parametrize("model_type", ["wan", "hunyuan"])
+@pytest.mark.parametrize("union", [False, True])
+def test_mask_from_lines_beyond_one_column_pass(model_type, union):
+    """nb > 2048 (256 threads x 8 columns): the kernel leaves its batched one-pass path and
+    walks the columns in passes; the second pass here holds 53-56 columns, a partial
+    thread and (hunyuan) the text columns."""
+    rng = np.random.default_rng(1234 + union)
+    H, n, bs, bpf, k = 3, 2101, 64, 30, 80
+    tb = 3 if model_type == "hunyuan" else 0
+    nb = n + tb
+    sel = rng.integers(0, 3 * n - 1, size=(H, k)).astype(np.int32)
+    modes = np.array([0, 1, 2], np.uint8)
+    st = {"block_size": bs, "text_token_num": tb * bs, "video_token_num": n * bs,
+          "model_type": model_type, "tile_rows": "union" if union else "exact"}
+    mask, tiles = md.attn_mask._generate_mask_and_tiles(
+        st, H, nb * bs, bpf, torch.from_numpy(sel).to(DEV),
+        torch.from_numpy(modes).to(DEV), torch.device(DEV))
+    ref = O.generate_mask_from_lines(sel, list(modes), seq_len=nb * bs, block_size=bs,
+                                     video_tokens=n * bs, text_tokens=tb * bs, bpf=bpf,
+                                     model_type=model_type)
+    got = mask.cpu().numpy()
+    assert got.shape == ref.shape and np.array_equal(got, ref)
+    c, lists = _tiles_np(tiles)
+    rc, rlists = O.tiles_from_mask(ref, bs, union)
+    assert np.array_equal(c, rc) and lists == rlists
+
+
 def _tiles_np(t: ops.TileList):
     c = t.counts.cpu().numpy()
     e = t.entries.cpu().numpy()
@@ -82,8 +109,9 @@ def _tiles_np(t: ops.TileList):
 
 
 @pytest.mark.parametrize("union", [False, True])
-@pytest.mark.parametrize("nb,bs", [(64, 64), (13, 64), (9, 128)])
+@pytest.mark.parametrize("nb,bs", [(64, 64), (13, 64), (9, 128), (2113, 64)])
 def test_mask_to_tiles_bit_exact(nb, bs, union):
+    """nb=2113 walks the mask's columns in two passes (the second holds 65)."""
     m = _random_block_mask(3, nb, 0.4, nb + bs)
     tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=union)
     c, lists = _tiles_np(tiles)
