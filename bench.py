@@ -833,6 +833,12 @@ def main(argv=None):
                                               q_video_offset=0, k_video_offset=0,
                                               video_blocks=N // bs, block_size=bs), 2)
     replay_ms = min(rp)
+    replay_board_ms, replay_board = sampled_loop(
+        lambda: ops.sparsity_map(q, k, lse, softmax_scale=D ** -0.5,
+                                 log_threshold=math.log(args.threshold), q_video_offset=0,
+                                 k_video_offset=0, video_blocks=N // bs, block_size=bs))
+    if replay_board is not None:
+        replay_board["ms_per_call"] = round(replay_board_ms, 3)
     # the single-kernel alternative (dense pass + map), for comparison only
     fm = time_events(lambda: ops.flash_fwd_map(q, k, v, softmax_scale=D ** -0.5,
                                                log_threshold=math.log(args.threshold),
@@ -898,6 +904,7 @@ def main(argv=None):
         "mask_overhead_ms": round(overhead_ms, 4),
         "mask_overhead_frac_of_dense": round(overhead_ms / dense_ms, 5),
         "replay_ms": round(replay_ms, 3),
+        "replay_board": replay_board,
         "map_step_ms": round(dense_ms + replay_ms, 3),
         "map_step_fused_ms": round(map_step_fused_ms, 3),
         "mask_overhead_amortized_ms": round(overhead_ms + replay_ms / 10.0, 4),
