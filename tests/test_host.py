@@ -212,3 +212,54 @@ def test_product_path_refuses_cpu_tensors():
     st = md.create_adaptive_mask_state("wan", 1, 256, 0, 128, 2, block_size=64)
     with pytest.raises(ValueError, match="GPU"):
         md.solve_lstsq(st, torch.zeros(1, 4, 4, dtype=torch.float16), 11, 2)
+
+
+def _fake_amdsmi(samples, cap_uw=1_400_000_000):
+    """A stand-in amdsmi module that serves `samples` (power W, clock MHz) in order."""
+    it = iter(samples)
+    calls = {"init": 0, "shutdown": 0}
+
+    def metrics(_h):
+        pw, clk = next(it, samples[-1])
+        return {"current_socket_power": pw, "current_gfxclk": clk}
+
+    m = types.SimpleNamespace(
+        amdsmi_init=lambda: calls.__setitem__("init", calls["init"] + 1),
+        amdsmi_shut_down=lambda: calls.__setitem__("shutdown", calls["shutdown"] + 1),
+        amdsmi_get_processor_handles=lambda: ["gpu0"],
+        amdsmi_get_power_cap_info=lambda _h: {"power_cap": cap_uw},
+        amdsmi_get_gpu_metrics_info=metrics)
+    return m, calls
+
+
+def test_board_sampler_drops_lagging_samples_and_sentinels(monkeypatch):
+    """bench.BoardSampler: samples inside the first skip_s seconds are dropped (the metrics
+    lag the load), 0xFFFF-style missing fields are ignored, amdsmi is shut down on exit."""
+    import sys
+    import time as _time
+
+    import bench
+
+    fake, calls = _fake_amdsmi([(0xFFFF, 1800)] * 3 + [(1300, 1850), (1320, 1870)] * 50)
+    monkeypatch.setitem(sys.modules, "amdsmi", fake)
+    with bench.BoardSampler(period_s=0.005, skip_s=0.02) as b:
+        _time.sleep(0.2)
+    r = b.result()
+    assert calls == {"init": 1, "shutdown": 1}
+    assert r is not None and r["samples"] >= 5
+    assert 1300 <= r["power_w"] <= 1320 and r["power_w_max"] == 1320
+    assert 1850 <= r["gfxclk_mhz"] <= 1870 and r["power_cap_w"] == 1400.0
+    kept = [x for x in b.samples if x[0] >= 0.02]
+    assert r["samples"] == len(kept) < len(b.samples)  # the earliest samples were dropped
+    assert all(x[1] != 0xFFFF for x in b.samples)      # sentinels never enter the record
+
+
+def test_board_sampler_without_amdsmi_reports_none(monkeypatch):
+    import sys
+
+    import bench
+
+    monkeypatch.setitem(sys.modules, "amdsmi", None)  # import raises ImportError
+    with bench.BoardSampler() as b:
+        pass
+    assert b.result() is None
