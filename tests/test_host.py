@@ -232,9 +232,9 @@ def _fake_amdsmi(samples, cap_uw=1_400_000_000):
     return m, calls
 
 
-def test_board_sampler_drops_lagging_samples_and_sentinels(monkeypatch):
-    """bench.BoardSampler: samples inside the first skip_s seconds are dropped (the metrics
-    lag the load), 0xFFFF-style missing fields are ignored, amdsmi is shut down on exit."""
+def test_board_sampler_collects_and_filters(monkeypatch):
+    """bench.BoardSampler on a stand-in amdsmi: 0xFFFF-style missing fields never enter the
+    record, amdsmi is initialised and shut down once, the cap is read in watts."""
     import sys
     import time as _time
 
@@ -242,16 +242,27 @@ def test_board_sampler_drops_lagging_samples_and_sentinels(monkeypatch):
 
     fake, calls = _fake_amdsmi([(0xFFFF, 1800)] * 3 + [(1300, 1850), (1320, 1870)] * 50)
     monkeypatch.setitem(sys.modules, "amdsmi", fake)
-    with bench.BoardSampler(period_s=0.005, skip_s=0.02) as b:
-        _time.sleep(0.2)
+    with bench.BoardSampler(period_s=0.005, skip_s=0.0) as b:
+        _time.sleep(0.1)
     r = b.result()
     assert calls == {"init": 1, "shutdown": 1}
-    assert r is not None and r["samples"] >= 5
-    assert 1300 <= r["power_w"] <= 1320 and r["power_w_max"] == 1320
+    assert r is not None and r["samples"] == len(b.samples) >= 2
+    assert all(x[1] != 0xFFFF for x in b.samples)
+    assert 1300 <= r["power_w"] <= 1320 and r["power_w_max"] <= 1320
     assert 1850 <= r["gfxclk_mhz"] <= 1870 and r["power_cap_w"] == 1400.0
-    kept = [x for x in b.samples if x[0] >= 0.02]
-    assert r["samples"] == len(kept) < len(b.samples)  # the earliest samples were dropped
-    assert all(x[1] != 0xFFFF for x in b.samples)      # sentinels never enter the record
+
+
+def test_board_sampler_result_drops_the_lag_window():
+    """Samples taken in the first skip_s seconds still show the load before the region."""
+    import bench
+
+    b = bench.BoardSampler(skip_s=1.0)
+    b.samples = [(0.0, 500.0, 900.0), (0.6, 900.0, 2300.0), (1.2, 1320.0, 1870.0),
+                 (1.7, 1330.0, 1860.0)]
+    r = b.result()
+    assert r["samples"] == 2 and r["power_w"] == 1325.0 and r["gfxclk_mhz"] == 1865
+    b.samples = [(0.2, 500.0, 900.0)]
+    assert b.result() is None
 
 
 def test_board_sampler_without_amdsmi_reports_none(monkeypatch):
