@@ -219,8 +219,11 @@ __global__ __launch_bounds__(kThreads, kRagged ? 2 : 3) __attribute__((amdgpu_wa
   auto decode = [&](int e_raw, int& kt, int& flags) {
     const int e = __builtin_amdgcn_readfirstlane(e_raw);
     kt = e >> 2;
+    // An entry outside the grid's key tiles [0, n_ktiles) holds no key of the sequence
+    // (a 128-token block mask on a sequence that ends in the first half of its last
+    // block lists such a tile): it is executed by no wave; its DMA loads a tile in range.
+    flags = (kt >= 0 && kt < p.n_ktiles) ? (e & 3) : 0;
     kt = kt < 0 ? 0 : (kt < p.n_ktiles ? kt : p.n_ktiles - 1);
-    flags = e & 3;
   };
   auto entry = [&](int i) -> int { return kSparse ? clist[i] : ((i << 2) | 3); };
 

@@ -168,6 +168,34 @@ def test_block_sparse_bs128_mask(dtype):
     _check_attn(out[0], ref, f"sparse bs128 {dtype}")
 
 
+@pytest.mark.parametrize("S", [1041, 1088, 1089])
+def test_block_sparse_bs128_tile_past_the_sequence_end(S):
+    """A 128-token block mask on a sequence that ends in the first half of its last block
+    (S mod 128 in 1..64) lists a 64-key tile wholly past the end. That entry holds no keys:
+    outputs equal those of the lists without it (bit for bit) and fp64 attention.
+    Regression: the kernels clamped the tile index and recomputed the last tile."""
+    H, D, bs = 2, 128, 128
+    nb = -(-S // bs)
+    q, k, v = (_randn((1, H, S, D), 640 + i, torch.bfloat16) for i in range(3))
+    m = _random_block_mask(H, nb, 0.5, 17)
+    m[:, :, nb - 1] = True  # every query tile lists the last block's two key tiles
+    full = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=False)
+    clipped = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=False,
+                                kv_tiles=-(-S // 64))
+    past = S % 128 and S % 128 <= 64
+    assert bool((full.counts > clipped.counts).any()) == bool(past)
+    o_full, l_full = ops.block_sparse_fwd(q, k, v, full, return_lse=True)
+    o_clip, l_clip = ops.block_sparse_fwd(q, k, v, clipped, return_lse=True)
+    assert torch.equal(o_full, o_clip) and torch.equal(l_full, l_clip)
+    tm = O.token_mask_from_blocks(m, bs)[:, :S, :S]
+    ref, _ = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), tm, dtype=np.float64)
+    _check_attn(o_full[0], ref, f"bs128 S={S}")
+    qz = ops.quantize_qkv(q, k, v)
+    o8_full, _ = ops.block_sparse_fwd_q8(qz, full)
+    o8_clip, _ = ops.block_sparse_fwd_q8(qz, clipped)
+    assert torch.equal(o8_full, o8_clip)
+
+
 @pytest.mark.parametrize("text,video,D,union,dtype", [
     (50, 450, 64, False, torch.bfloat16), (50, 450, 128, True, torch.bfloat16),
     (226, 1350, 64, False, torch.bfloat16), (100, 200, 128, False, torch.bfloat16),
