@@ -7,7 +7,14 @@ tile rows, mask density and, for text-first layouts, a shifted block grid. It ch
   the north-star bound (max-abs <= 2e-2, mean-abs <= 2e-3) and an LSE bound of 2e-3;
 - the int8/fp8 block-sparse kernel against the oracle's model of its arithmetic (the
   bounds of tests/test_gpu_q8.py: 4e-3 max-abs, 3e-4 mean-abs, 2e-4 on the LSE);
-- masks and tile lists generated from selected lines, bit-exactly.
+- masks and tile lists generated from selected lines, bit-exactly;
+- the replay map of exact (quarter-integer) scores against the oracle's replay of the
+  same LSE, bit-exactly, for the wan, hunyuan and cogvideox layouts (partial last video
+  blocks included), batches of 1-2;
+- the fused dense + map kernel against the separate replay of its own LSE (bit-exact)
+  and fp64 attention;
+- M^T S on arbitrary finite fp16 (bit-exact), the fit against the fp64 ridge solution
+  (2e-6 of max|X|), and line selection with ties, signed zeros and NaN (bit-exact).
 
 The draws are fixed by the case index, so a failure names a reproducible configuration.
 """
@@ -156,3 +163,140 @@ def test_random_mask_from_lines_bit_exact(i):
     c_got = tiles.counts.cpu().numpy()
     assert np.array_equal(c_got, c_ref), tag
     assert _lists(tiles) == [[[int(x) for x in t] for t in h] for h in l_ref], tag
+
+
+# ---------------------------------------------------------------- replay map / fused pass
+def _draw_map(i):
+    rng = np.random.default_rng(11000 + i)
+    model_type = ["wan", "hunyuan", "cogvideox"][int(rng.integers(0, 3))]
+    bs = int(rng.choice([64, 128]))
+    D = int(rng.choice([64, 128]))
+    dtype = [torch.bfloat16, torch.float16][int(rng.integers(0, 2))]
+    if model_type == "wan":
+        text, video = 0, bs * int(rng.integers(2, 9))
+    elif model_type == "hunyuan":
+        text, video = int(rng.integers(1, 2 * bs)), bs * int(rng.integers(2, 9))
+    else:  # text first; the video may end in a partial block
+        text, video = int(rng.integers(1, 2 * bs)), int(rng.integers(2 * bs, 9 * bs))
+    S = text + video
+    B = int(rng.integers(1, 3))
+    H = int(rng.integers(1, 3))
+    # scores exact in fp32: multiples of 1/4 in [-2, 2] (d=64 and d=128 alike)
+    qn = rng.integers(-8, 9, size=(B, H, S, D)).astype(np.float32) / 4
+    kn = rng.integers(-8, 9, size=(B, H, S, D)).astype(np.float32) / 4
+    thr = float(rng.choice([1e-2, 1e-3, 1e-4]))
+    return dict(model_type=model_type, bs=bs, D=D, dtype=dtype, text=text, video=video, S=S,
+                B=B, H=H, qn=qn, kn=kn, thr=thr)
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_random_replay_map_bit_exact(i):
+    """The replay map of exact scores against the oracle's replay of the same LSE."""
+    import math
+
+    c = _draw_map(i)
+    tag = (f"case {i}: {c['model_type']} bs={c['bs']} D={c['D']} {c['dtype']} text={c['text']} "
+           f"video={c['video']} B={c['B']} H={c['H']} thr={c['thr']}")
+    print(tag, flush=True)
+    q = torch.from_numpy(c["qn"]).to(c["dtype"]).to(DEV)
+    k = torch.from_numpy(c["kn"]).to(c["dtype"]).to(DEV)
+    D, bs = c["D"], c["bs"]
+    scale = D ** -0.5
+    s = np.einsum("bhqd,bhkd->bhqk", c["qn"].astype(np.float64), c["kn"].astype(np.float64)) * scale
+    lse = np.log(np.exp(s).sum(-1)).astype(np.float32)
+    vb, qo, ko = O.video_layout(c["model_type"], c["S"], c["video"], c["text"], bs)
+    ln_thr = math.log(c["thr"])
+    got = md.cuda_sparsity_map(q, k, torch.from_numpy(lse).to(DEV), softmax_scale=scale,
+                               log_threshold=ln_thr, q_video_offset=qo, k_video_offset=ko,
+                               video_blocks=vb, block_size=bs)
+    dt = "bf16" if c["dtype"] == torch.bfloat16 else "fp16"
+    for b in range(c["B"]):
+        ref = O.replay_map(c["qn"][b], c["kn"][b], lse[b], scale=scale, log_threshold=ln_thr,
+                           q_off=qo, k_off=ko, video_blocks=vb, block_size=bs, dtype=dt)
+        assert np.array_equal(got[b].cpu().numpy(), ref), (tag, b)
+
+
+@pytest.mark.parametrize("i", range(6))
+def test_random_fused_map_pass_equals_two_kernels(i):
+    """The fused dense + map kernel: the map equals the separate replay of its own LSE."""
+    import math
+
+    c = _draw_map(100 + i)
+    tag = (f"case {i}: {c['model_type']} bs={c['bs']} D={c['D']} {c['dtype']} text={c['text']} "
+           f"video={c['video']} B={c['B']} H={c['H']}")
+    print(tag, flush=True)
+    q = torch.from_numpy(c["qn"]).to(c["dtype"]).to(DEV)
+    k = torch.from_numpy(c["kn"]).to(c["dtype"]).to(DEV)
+    v = _randn(tuple(q.shape), 12000 + i, c["dtype"])
+    vb, qo, _ = O.video_layout(c["model_type"], c["S"], c["video"], c["text"], c["bs"])
+    scale = c["D"] ** -0.5
+    ln_thr = math.log(c["thr"])
+    out, lse, smap = ops.flash_fwd_map(q, k, v, softmax_scale=scale, log_threshold=ln_thr,
+                                       video_offset=qo, video_blocks=vb, block_size=c["bs"])
+    sep = md.cuda_sparsity_map(q, k, lse, softmax_scale=scale, log_threshold=ln_thr,
+                               q_video_offset=qo, k_video_offset=qo, video_blocks=vb,
+                               block_size=c["bs"])
+    assert torch.equal(sep, smap), tag
+    for b in range(c["B"]):
+        ref, ref_lse = O.masked_attention(c["qn"][b], c["kn"][b], _np(v[b]), None,
+                                          dtype=np.float64)
+        err = np.abs(_np(out[b]).astype(np.float64) - ref)
+        assert err.max() <= 2e-2 and err.mean() <= 2e-3, (tag, b, err.max(), err.mean())
+        np.testing.assert_allclose(_np(lse[b]), ref_lse, rtol=0, atol=2e-3)
+
+
+# ---------------------------------------------------------------- M^T S, fit, selection
+@pytest.mark.parametrize("i", range(10))
+def test_random_mts_bit_exact(i):
+    rng = np.random.default_rng(13000 + i)
+    n = int(rng.integers(2, 900))
+    bpf = int(rng.integers(1, max(2, n // 2)))
+    H = int(rng.integers(1, 4))
+    print(f"case {i}: n={n} bpf={bpf} H={H}", flush=True)
+    bits = rng.integers(0, 0x7C00, size=(H, n, n)).astype(np.uint16)
+    bits |= (rng.integers(0, 2, size=bits.shape) << 15).astype(np.uint16)
+    S = bits.view(np.float16)
+    got = md.compute_mts(torch.from_numpy(S.copy()).to(DEV), bpf).cpu().numpy()
+    assert np.array_equal(got, O.mts_exact(S, bpf)), (n, bpf, H)
+
+
+@pytest.mark.parametrize("i", range(6))
+def test_random_fit_matches_fp64_ridge(i):
+    rng = np.random.default_rng(14000 + i)
+    bpf = int(rng.integers(2, 40))
+    frames = int(rng.integers(2, 12))
+    n = bpf * frames
+    H = int(rng.integers(1, 5))
+    print(f"case {i}: n={n} bpf={bpf} H={H}", flush=True)
+    S = (rng.integers(0, 4097, size=(H, n, n)) / 4096.0).astype(np.float16)
+    st = md.create_adaptive_mask_state("wan", H, n * 64, 0, bpf * 64, frames, block_size=64)
+    feats = md.solve_lstsq(st, torch.from_numpy(S).to(DEV), step=st["warmup_steps"],
+                           blocks_per_frame=bpf, regularization=1.0)
+    X = O.ridge_solve(S.astype(np.float64), bpf, 1.0)
+    got = feats["_x"].cpu().numpy().astype(np.float64)
+    err = np.abs(got - X).max() / np.abs(X).max()
+    print(f"  max err / max|X| = {err:.3e}", flush=True)
+    assert err <= 2e-6, (n, bpf, H, err)
+
+
+@pytest.mark.parametrize("i", range(10))
+def test_random_select_lines_bit_exact(i):
+    rng = np.random.default_rng(15000 + i)
+    n = int(rng.integers(2, 700))
+    k = int(rng.integers(1, 3 * n + 20))
+    T = int(rng.integers(1, 20))
+    H = int(rng.integers(1, 6))
+    print(f"case {i}: n={n} k={k} T={T} H={H}", flush=True)
+    xc = rng.normal(size=(H, 3 * n)).astype(np.float32)
+    xl = rng.normal(size=(H, 3 * n)).astype(np.float32)
+    # ties (quantised values), signed zeros and a NaN
+    if rng.random() < 0.5:
+        xc = np.round(xc * 4) / 4
+        xl = np.round(xl * 4) / 4
+    xc[0, int(rng.integers(0, 3 * n))] = 0.0
+    xl[0, int(rng.integers(0, 3 * n))] = -0.0
+    if rng.random() < 0.3:
+        xc[H - 1, int(rng.integers(0, 3 * n))] = np.nan
+    got = ops.select_lines(torch.from_numpy(xc).to(DEV), torch.from_numpy(xl).to(DEV), n, T, k)
+    ref = O.choose_topk_lines(xc, xl, n, T, k)
+    assert np.array_equal(got.cpu().numpy(), ref), (n, k, T, H)
