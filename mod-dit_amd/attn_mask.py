@@ -259,7 +259,18 @@ def _engine(query, key, value, mask, tiles, pre_defined_mask, video_token_num, b
         mask = mask.unsqueeze(0).expand(query.shape[1], -1, -1)
     q8 = precision == "int8"
     if pre_defined_mask is None:
-        if tiles is None:
+        if block_size == 128 and grid_origin <= -64:
+            # The kernels run 64-key tiles on a grid that starts in (-64, 0]. A 128-block
+            # grid starting 64..127 tokens before token 0 is the 64-tile grid 64 tokens
+            # later with its first tile row and column all padding. Each 128-block row
+            # keeps its own mask on both of its 64-row halves (exact rows), so the token
+            # mask is the same.
+            grid_origin += 64
+            n64 = -(-(query.shape[2] - grid_origin) // 64)  # tiles the sequence reaches
+            m64 = mask.repeat_interleave(2, dim=1).repeat_interleave(2, dim=2)
+            m64 = m64[:, 1:n64 + 1, 1:n64 + 1]
+            tiles = ops.mask_to_tiles(m64, 64, union_rows=False, grid_origin=grid_origin)
+        elif tiles is None:
             tiles = ops.mask_to_tiles(mask, block_size, union_rows=union_rows,
                                       grid_origin=grid_origin)
         if q8:

@@ -300,3 +300,73 @@ def test_random_select_lines_bit_exact(i):
     got = ops.select_lines(torch.from_numpy(xc).to(DEV), torch.from_numpy(xl).to(DEV), n, T, k)
     ref = O.choose_topk_lines(xc, xl, n, T, k)
     assert np.array_equal(got.cpu().numpy(), ref), (n, k, T, H)
+
+
+# ---------------------------------------------------------------- whole schedules
+@pytest.mark.parametrize("i", range(8))
+def test_random_schedule_sparse_steps(i):
+    """SparseAttentionWithMap over W-2 .. W+T+1 (map, fit, predict, sparse, refresh,
+    sparse) on a random wan or text-first cogvideox layer. Every sparse step's output is
+    checked against fp64 attention (bf16) or the oracle's model of the quantised
+    arithmetic (int8) under the mask the state holds, as the kernels execute it; every
+    map step's output against fp64 dense attention."""
+    rng = np.random.default_rng(16000 + i)
+    model_type = ["wan", "cogvideox"][int(rng.integers(0, 2))]
+    bs = int(rng.choice([64, 128]))
+    tile_rows = ["exact", "union"][int(rng.integers(0, 2))]
+    precision = ["bf16", "int8"][int(rng.integers(0, 2))]
+    H = int(rng.integers(1, 4))
+    D = int(rng.choice([64, 128]))
+    F = int(rng.integers(2, 5))
+    if model_type == "wan":
+        text, tpf = 0, bs * int(rng.integers(2, 7))
+    else:
+        text, tpf = int(rng.integers(1, 150)), int(rng.integers(bs, 5 * bs))
+    video = F * tpf
+    S = text + video
+    W, T = int(rng.integers(3, 6)), int(rng.integers(2, 4))
+    n_v = -(-video // bs)
+    top_k = int(rng.integers(1, max(2, 3 * n_v // 2)))
+    origin = O.cogvideox_grid(text, video, bs)[2] if model_type == "cogvideox" else 0
+    tag = (f"case {i}: {model_type} bs={bs} {tile_rows} {precision} H={H} D={D} F={F} "
+           f"tpf={tpf} text={text} W={W} T={T} top_k={top_k}")
+    print(tag, flush=True)
+    st = md.create_adaptive_mask_state(model_type, H, video, text, tpf, F, warmup_steps=W,
+                                       top_k=top_k, predict_T=T, threshold=1e-3,
+                                       block_size=bs, tile_rows=tile_rows, precision=precision)
+    base = [torch.randn(1, H, S, D, generator=torch.Generator().manual_seed(17000 + 10 * i + j))
+            for j in range(3)]
+    checked = 0
+    for step in range(W - 2, W + T + 2):
+        g = torch.Generator().manual_seed(18000 + 100 * i + step)
+        q, k, v = ((b + 0.3 * torch.randn(b.shape, generator=g)).to(torch.bfloat16).to(DEV)
+                   for b in base)
+        phase = O.step_phase(step, W, T)
+        out, _ = md.SparseAttentionWithMap(q, k, v, st, None, current_step=step)
+        qn, kn, vn = _np(q[0]), _np(k[0]), _np(v[0])
+        if phase != "sparse":
+            ref, _ = O.masked_attention(qn, kn, vn, None, dtype=np.float64)
+            err = np.abs(_np(out[0]).astype(np.float64) - ref)
+            assert err.max() <= 2e-2 and err.mean() <= 2e-3, (tag, step, phase, err.max())
+            continue
+        mask = st["mask"].cpu().numpy()
+        _, lists = O.tiles_from_mask(mask, bs, tile_rows == "union")
+        tm = O.token_mask_from_tiles(lists, H, S, S, origin=origin)
+        if precision == "int8":
+            qz = ops.quantize_qkv(q, k, v, grid_origin=origin)
+            zn = dict(q8=qz.q8[0].cpu().numpy(), q_scale=qz.q_scale[0].cpu().numpy(),
+                      k8=qz.k8[0].cpu().numpy(), k_scale=qz.k_scale[0].cpu().numpy(),
+                      v8t=qz.v8t[0].cpu().numpy(), v_scale=qz.v_scale[0].cpu().numpy(),
+                      k_mean=qz.k_mean[0].cpu().numpy(), q_kmean=qz.q_kmean[0].cpu().numpy())
+            ref, _ = O.attention_q8(zn, tm, origin=origin)
+            err = np.abs(_np(out[0]).astype(np.float64) - ref)
+            assert err.max() <= 4e-3 and err.mean() <= 3e-4, (tag, step, err.max(), err.mean())
+        else:
+            ref, _ = O.masked_attention(qn, kn, vn, tm, dtype=np.float64)
+            err = np.abs(_np(out[0]).astype(np.float64) - ref)
+            bound = 2e-2 + (2.0 ** -9) * np.abs(ref)  # half a bf16 ulp where |o| is large
+            assert np.all(err <= bound) and err.mean() <= 2e-3, (tag, step, err.max(), err.mean())
+        print(f"  sparse step {step}: max-abs {err.max():.3e} mean-abs {err.mean():.3e}",
+              flush=True)
+        checked += 1
+    assert checked >= 2, tag

@@ -286,3 +286,47 @@ def test_use_dense_and_error_paths():
     st2 = md.create_adaptive_mask_state("wan", H, S, 0, 128, 2, sparse_type="radial")
     with pytest.raises(NotImplementedError):
         md.SparseAttentionWithMap(q, k, v, st2, None, current_step=20)
+
+
+@pytest.mark.parametrize("precision", ["bf16", "int8"])
+def test_cogvideox_128_blocks_grid_starting_beyond_64_tokens(precision):
+    """Text-first layout with 128-token blocks and 130 text tokens: the padded grid starts
+    126 tokens before token 0, beyond the (-64, 0] the kernels' 64-tile grids take. The
+    engine runs the equivalent 64-tile grid (origin -62, first tile row and column all
+    padding). Sparse steps must match attention under the 128-block mask on the -126 grid.
+    Regression: the sparse steps raised on the grid origin."""
+    H, D, bs, text, F, tpf = 2, 64, 128, 130, 3, 300
+    video = F * tpf
+    S = text + video
+    W, T = 4, 3
+    tb, vb, origin = O.cogvideox_grid(text, video, bs)
+    assert origin == -126
+    st = md.create_adaptive_mask_state("cogvideox", H, video, text, tpf, F, warmup_steps=W,
+                                       top_k=8, predict_T=T, threshold=1e-3, block_size=bs,
+                                       tile_rows="exact", precision=precision)
+    checked = 0
+    for step in range(W - 2, W + 2):
+        g = torch.Generator().manual_seed(90 + step)
+        q, k, v = (torch.randn(1, H, S, D, generator=g).to(torch.bfloat16).to(DEV)
+                   for _ in range(3))
+        out, _ = md.SparseAttentionWithMap(q, k, v, st, None, current_step=step)
+        if O.step_phase(step, W, T) != "sparse":
+            continue
+        mask = st["mask"].cpu().numpy()
+        assert mask.shape == (H, tb + vb, tb + vb)
+        _, lists = O.tiles_from_mask(mask, bs, False)
+        tm = O.token_mask_from_tiles(lists, H, S, S, origin=origin)
+        if precision == "bf16":
+            ref, _ = O.masked_attention(_np(q[0]), _np(k[0]), _np(v[0]), tm, dtype=np.float64)
+            _check_attn(out[0], ref, f"cogvideox bs=128 origin={origin} step {step}", sparse=True)
+        else:
+            qz = ops.quantize_qkv(q, k, v, grid_origin=origin + 64)
+            zn = dict(q8=qz.q8[0].cpu().numpy(), q_scale=qz.q_scale[0].cpu().numpy(),
+                      k8=qz.k8[0].cpu().numpy(), k_scale=qz.k_scale[0].cpu().numpy(),
+                      v8t=qz.v8t[0].cpu().numpy(), v_scale=qz.v_scale[0].cpu().numpy(),
+                      k_mean=qz.k_mean[0].cpu().numpy(), q_kmean=qz.q_kmean[0].cpu().numpy())
+            ref, _ = O.attention_q8(zn, tm, origin=origin + 64)
+            err = np.abs(_np(out[0]).astype(np.float64) - ref)
+            assert err.max() <= 4e-3 and err.mean() <= 3e-4, (step, err.max(), err.mean())
+        checked += 1
+    assert checked == 2
