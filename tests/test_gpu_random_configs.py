@@ -6,7 +6,8 @@ tile rows, mask density and, for text-first layouts, a shifted block grid. It ch
 - dense and block-sparse attention against fp64 attention under the executed mask, to
   the north-star bound (max-abs <= 2e-2, mean-abs <= 2e-3) and an LSE bound of 2e-3;
 - the int8/fp8 block-sparse kernel against the oracle's model of its arithmetic (the
-  bounds of tests/test_gpu_q8.py: 4e-3 max-abs, 3e-4 mean-abs, 2e-4 on the LSE);
+  bounds of tests/test_gpu_q8.py: 4e-3 max-abs, 3e-4 mean-abs, 2e-4 on the LSE; rare
+  e4m3 rounding-boundary elements up to 2e-2, see _check_q8_model);
 - masks and tile lists generated from selected lines, bit-exactly;
 - the replay map of exact (quarter-integer) scores against the oracle's replay of the
   same LSE, bit-exactly, for the wan, hunyuan and cogvideox layouts (partial last video
@@ -14,7 +15,10 @@ tile rows, mask density and, for text-first layouts, a shifted block grid. It ch
 - the fused dense + map kernel against the separate replay of its own LSE (bit-exact)
   and fp64 attention;
 - M^T S on arbitrary finite fp16 (bit-exact), the fit against the fp64 ridge solution
-  (2e-6 of max|X|), and line selection with ties, signed zeros and NaN (bit-exact).
+  (2e-6 of max|X|), and line selection with ties, signed zeros and NaN (bit-exact);
+- whole SparseAttentionWithMap schedules (W-2 .. W+T+1) on random wan, text-first
+  cogvideox and hunyuan (padding mask) layers in bf16 and int8: every step's output
+  against fp64 attention or the quantised oracle under the mask the state holds.
 
 The draws are fixed by the case index, so a failure names a reproducible configuration.
 """
@@ -43,6 +47,21 @@ def _lists(tiles):
     c = tiles.counts.cpu().numpy()
     e = tiles.entries.cpu().numpy()
     return [[[int(x) for x in e[h, t, :c[h, t]]] for t in range(c.shape[1])] for h in range(c.shape[0])]
+
+
+def _check_q8_model(err, tag):
+    """The int8/fp8 kernel against the oracle's fp64 model of its arithmetic: 4e-3 max-abs
+    and 3e-4 mean-abs (tests/test_gpu_q8.py), except where a weight P lies on an e4m3
+    rounding boundary and the kernel (fp32 exp2) and the model (fp64) round it one code
+    apart: 2^-3 relative, which moves O by up to w |v| / 8 for a dominant weight w. Such
+    elements must be rare (at most 1e-5 of the output, at least one allowed) and stay
+    within 2e-2."""
+    n_over = int((err > 4e-3).sum())
+    print(f"  q8 vs model: max-abs {err.max():.3e} mean-abs {err.mean():.3e} "
+          f"above 4e-3: {n_over} of {err.size}", flush=True)
+    assert err.mean() <= 3e-4, (tag, err.mean())
+    assert err.max() <= 2e-2, (tag, err.max())
+    assert n_over <= max(1, int(1e-5 * err.size)), (tag, n_over)
 
 
 def _draw_attention(i):
@@ -123,8 +142,7 @@ def test_random_int8_block_sparse_against_quantised_oracle(i):
     tm = O.token_mask_from_tiles(_lists(tiles), H, S, S, origin=c["origin"])
     ref, ref_lse = O.attention_q8(zn, tm, origin=c["origin"])
     err = np.abs(_np(out[0]).astype(np.float64) - ref)
-    print(f"  q8 max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
-    assert err.max() <= 4e-3 and err.mean() <= 3e-4, (tag, err.max(), err.mean())
+    _check_q8_model(err, tag)
     got_lse = _np(lse[0])
     fin = np.isfinite(ref_lse)
     assert np.array_equal(np.isfinite(got_lse), fin), tag
@@ -303,7 +321,7 @@ def test_random_select_lines_bit_exact(i):
 
 
 # ---------------------------------------------------------------- whole schedules
-@pytest.mark.parametrize("i", range(8))
+@pytest.mark.parametrize("i", range(16))
 def test_random_schedule_sparse_steps(i):
     """SparseAttentionWithMap over W-2 .. W+T+1 (map, fit, predict, sparse, refresh,
     sparse) on a random wan or text-first cogvideox layer. Every sparse step's output is
@@ -353,14 +371,16 @@ def test_random_schedule_sparse_steps(i):
         _, lists = O.tiles_from_mask(mask, bs, tile_rows == "union")
         tm = O.token_mask_from_tiles(lists, H, S, S, origin=origin)
         if precision == "int8":
-            qz = ops.quantize_qkv(q, k, v, grid_origin=origin)
+            # the kernels' 64-tile grid: 64 tokens later when 128-blocks start >= 64 early
+            grid = origin + 64 if bs == 128 and origin <= -64 else origin
+            qz = ops.quantize_qkv(q, k, v, grid_origin=grid)
             zn = dict(q8=qz.q8[0].cpu().numpy(), q_scale=qz.q_scale[0].cpu().numpy(),
                       k8=qz.k8[0].cpu().numpy(), k_scale=qz.k_scale[0].cpu().numpy(),
                       v8t=qz.v8t[0].cpu().numpy(), v_scale=qz.v_scale[0].cpu().numpy(),
                       k_mean=qz.k_mean[0].cpu().numpy(), q_kmean=qz.q_kmean[0].cpu().numpy())
-            ref, _ = O.attention_q8(zn, tm, origin=origin)
+            ref, _ = O.attention_q8(zn, tm, origin=grid)
             err = np.abs(_np(out[0]).astype(np.float64) - ref)
-            assert err.max() <= 4e-3 and err.mean() <= 3e-4, (tag, step, err.max(), err.mean())
+            _check_q8_model(err, (tag, step))
         else:
             ref, _ = O.masked_attention(qn, kn, vn, tm, dtype=np.float64)
             err = np.abs(_np(out[0]).astype(np.float64) - ref)
@@ -370,3 +390,80 @@ def test_random_schedule_sparse_steps(i):
               flush=True)
         checked += 1
     assert checked >= 2, tag
+
+
+@pytest.mark.parametrize("i", range(10))
+def test_random_hunyuan_schedule_with_padding_mask(i):
+    """Hunyuan layout (video first, a text tail of which only the first tokens are valid,
+    the processor's padding mask): dense steps over the valid keys, map steps without the
+    padding mask, sparse steps with video rows block-sparse over the key tiles below
+    ceil(valid/64) and text rows dense over the valid keys."""
+    rng = np.random.default_rng(19000 + i)
+    bs = int(rng.choice([64, 128]))
+    tile_rows = ["exact", "union"][int(rng.integers(0, 2))]
+    precision = ["bf16", "int8"][int(rng.integers(0, 2))]
+    H = int(rng.integers(1, 4))
+    D = int(rng.choice([64, 128]))
+    F = int(rng.integers(2, 4))
+    tpf = bs * int(rng.integers(2, 6))
+    video = F * tpf
+    text = bs * int(rng.integers(1, 4))
+    valid = video + int(rng.integers(0, text + 1))
+    S = video + text
+    W, T = int(rng.integers(3, 6)), int(rng.integers(2, 4))
+    top_k = int(rng.integers(1, max(2, 3 * (video // bs) // 2)))
+    tag = (f"case {i}: bs={bs} {tile_rows} {precision} H={H} D={D} F={F} tpf={tpf} "
+           f"text={text} valid={valid} W={W} T={T} top_k={top_k}")
+    print(tag, flush=True)
+    st = md.create_adaptive_mask_state("hunyuan", H, video, text, tpf, F, warmup_steps=W,
+                                       top_k=top_k, predict_T=T, threshold=1e-3,
+                                       block_size=bs, tile_rows=tile_rows, precision=precision)
+    pdm = torch.zeros(S, S, dtype=torch.bool, device=DEV)
+    pdm[:, :valid] = True
+    checked = 0
+    for step in range(W + T + 1):
+        g = torch.Generator().manual_seed(20000 + 100 * i + step)
+        q, k, v = (torch.randn(1, H, S, D, generator=g).to(torch.bfloat16).to(DEV)
+                   for _ in range(3))
+        qn, kn, vn = _np(q[0]), _np(k[0]), _np(v[0])
+        phase = O.step_phase(step, W, T)
+        out, _ = md.SparseAttentionWithMap(q, k, v, st, None, pre_defined_mask=pdm,
+                                           current_step=step, use_dense=step < W - 2)
+        if phase == "dense":
+            tm = np.zeros((H, S, S), bool)
+            tm[:, :, :valid] = True
+            ref, _ = O.masked_attention(qn, kn, vn, tm, dtype=np.float64)
+        elif phase != "sparse":
+            ref, _ = O.masked_attention(qn, kn, vn, None, dtype=np.float64)
+        if phase != "sparse":
+            err = np.abs(_np(out[0]).astype(np.float64) - ref)
+            assert err.max() <= 2e-2 and err.mean() <= 2e-3, (tag, step, phase, err.max())
+            continue
+        mask = st["mask"].cpu().numpy()
+        nbv = video // bs
+        kv_tiles = (valid + 63) // 64
+        _, lists = O.tiles_from_mask(mask[:, :nbv, :], bs, tile_rows == "union",
+                                     kv_tiles=kv_tiles)
+        tm = np.zeros((H, S, S), bool)
+        tm[:, :video, :] = O.token_mask_from_tiles(lists, H, video, S)
+        tm[:, video:, :valid] = True
+        ref, _ = O.masked_attention(qn, kn, vn, tm, dtype=np.float64)
+        got = _np(out[0]).astype(np.float64)
+        err_text = np.abs(got[:, video:] - ref[:, video:])
+        assert err_text.max() <= 2e-2 and err_text.mean() <= 2e-3, (tag, step, "text rows")
+        if precision == "int8":
+            qz = ops.quantize_qkv(q, k, v)
+            zn = dict(q8=qz.q8[0].cpu().numpy(), q_scale=qz.q_scale[0].cpu().numpy(),
+                      k8=qz.k8[0].cpu().numpy(), k_scale=qz.k_scale[0].cpu().numpy(),
+                      v8t=qz.v8t[0].cpu().numpy(), v_scale=qz.v_scale[0].cpu().numpy(),
+                      k_mean=qz.k_mean[0].cpu().numpy(), q_kmean=qz.q_kmean[0].cpu().numpy())
+            ref_q, _ = O.attention_q8(zn, tm)
+            err = np.abs(got[:, :video] - ref_q[:, :video])
+            _check_q8_model(err, (tag, step))
+        else:
+            err = np.abs(got[:, :video] - ref[:, :video])
+            bound = 2e-2 + (2.0 ** -9) * np.abs(ref[:, :video])
+            assert np.all(err <= bound) and err.mean() <= 2e-3, (tag, step, err.max(), err.mean())
+        print(f"  sparse step {step}: video max-abs {err.max():.3e}", flush=True)
+        checked += 1
+    assert checked >= 1, tag
