@@ -16,6 +16,8 @@ tile rows, mask density and, for text-first layouts, a shifted block grid. It ch
   and fp64 attention;
 - M^T S on arbitrary finite fp16 (bit-exact), the fit against the fp64 ridge solution
   (2e-6 of max|X|), and line selection with ties, signed zeros and NaN (bit-exact);
+- batches of 1-3 in both input layouts with strided outputs, and dense attention with
+  different query and key lengths;
 - whole SparseAttentionWithMap schedules (W-2 .. W+T+1) on random wan, text-first
   cogvideox and hunyuan (padding mask) layers in bf16 and int8: every step's output
   against fp64 attention or the quantised oracle under the mask the state holds.
@@ -467,3 +469,53 @@ def test_random_hunyuan_schedule_with_padding_mask(i):
         print(f"  sparse step {step}: video max-abs {err.max():.3e}", flush=True)
         checked += 1
     assert checked >= 1, tag
+
+
+# ---------------------------------------------------------------- batches, layouts, lengths
+@pytest.mark.parametrize("i", range(10))
+def test_random_batches_layouts_and_cross_lengths(i):
+    """Batches of 1-3 in (B,H,S,D) or the processors' (B,S,H,D)-strided layout, outputs
+    into strided views; dense attention with a key length different from the query
+    length; block-sparse with one per-head mask shared by the batch (every batch element
+    checked on its own against fp64 under the executed mask)."""
+    rng = np.random.default_rng(21000 + i)
+    B = int(rng.integers(1, 4))
+    H = int(rng.integers(1, 4))
+    D = int(rng.choice([64, 128]))
+    dtype = [torch.bfloat16, torch.float16][int(rng.integers(0, 2))]
+    Sq = int(rng.integers(1, 1500))
+    Skv = int(rng.integers(1, 1500))
+    bshd = bool(rng.integers(0, 2))
+    tag = f"case {i}: B={B} H={H} D={D} {dtype} Sq={Sq} Skv={Skv} bshd={bshd}"
+    print(tag, flush=True)
+    g = torch.Generator().manual_seed(22000 + i)
+
+    def make(S):
+        if bshd:
+            return torch.randn((B, S, H, D), generator=g).to(dtype).to(DEV).transpose(1, 2)
+        return torch.randn((B, H, S, D), generator=g).to(dtype).to(DEV)
+
+    q, k, v = make(Sq), make(Skv), make(Skv)
+    out_store = torch.full((B, Sq, H, D), float("nan"), dtype=dtype, device=DEV)
+    out, lse = ops.flash_fwd(q, k, v, out=out_store.transpose(1, 2))
+    assert not torch.isnan(out).any(), tag
+    for b in range(B):
+        ref, ref_lse = O.masked_attention(_np(q[b]), _np(k[b]), _np(v[b]), None, dtype=np.float64)
+        err = np.abs(_np(out[b]).astype(np.float64) - ref)
+        assert err.max() <= 2e-2 and err.mean() <= 2e-3, (tag, "dense", b, err.max())
+        np.testing.assert_allclose(_np(lse[b]), ref_lse, rtol=0, atol=2e-3)
+    # block-sparse self-attention on the query tensor's length, mask shared by the batch
+    S = Sq
+    k2, v2 = make(S), make(S)
+    bs = int(rng.choice([64, 128]))
+    nb = -(-S // bs)
+    m = rng.random((H, nb, nb)) < float(rng.uniform(0.1, 0.8))
+    union = bool(rng.integers(0, 2))
+    tiles = ops.mask_to_tiles(torch.from_numpy(m).to(DEV), bs, union_rows=union)
+    out2_store = torch.full((B, S, H, D), float("nan"), dtype=dtype, device=DEV)
+    out2, _ = ops.block_sparse_fwd(q, k2, v2, tiles, out=out2_store.transpose(1, 2))
+    tm = O.token_mask_from_tiles(_lists(tiles), H, S, S)
+    for b in range(B):
+        ref, _ = O.masked_attention(_np(q[b]), _np(k2[b]), _np(v2[b]), tm, dtype=np.float64)
+        err = np.abs(_np(out2[b]).astype(np.float64) - ref)
+        assert err.max() <= 2e-2 and err.mean() <= 2e-3, (tag, "sparse", b, err.max())
