@@ -923,9 +923,9 @@ def main(argv=None):
             "mfma_ceiling": ceiling,
             "frac_of_mfma_ceiling": (round(achieved / ceiling["value"], 4) if ceiling else None),
             "board": board,
-            # the same peak at the clock the board held under this call (BASELINE.md's
-            # "fraction of the bf16 MFMA peak computed from the measured clock"); amdsmi's
-            # gfx clock reads ~2.5 % above the shader-cycle clock, so this errs low
+            # the fraction of the bf16 MFMA peak computed from the measured clock: the same
+            # peak at the clock the board held under this call; amdsmi's gfx clock reads
+            # ~2.5 % above the shader-cycle clock, so this errs low
             "peak_at_measured_clock": (round(MI355X_BF16_FLOP_PER_CYCLE * board["gfxclk_mhz"] * 1e6
                                              / 1e12, 1) if board else None),
             "frac_at_measured_clock": (round(achieved / (MI355X_BF16_FLOP_PER_CYCLE
