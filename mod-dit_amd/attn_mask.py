@@ -195,6 +195,8 @@ def _generate_mask_and_tiles(warmup_state: Dict, num_heads: int, n: int, blocks_
     modes = _mode_tensor(mode, num_heads, device)
     union = warmup_state.get("tile_rows", "union") == "union"
     n_video = max(video_block_num, 1)
+    if block_size == 128 and origin <= -64:
+        want_tiles = False  # the engine runs such grids on 64-token tiles (see _engine)
     return ops.mask_from_lines(selected_lines, modes, n=n_video,
                                blocks_per_frame=max(int(blocks_per_frame), 1), layout=layout,
                                nb=nb, text_blocks=text_block_num, block_size=block_size,
