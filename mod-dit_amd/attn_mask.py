@@ -196,7 +196,7 @@ def _generate_mask_and_tiles(warmup_state: Dict, num_heads: int, n: int, blocks_
     union = warmup_state.get("tile_rows", "union") == "union"
     n_video = max(video_block_num, 1)
     if block_size == 128 and origin <= -64:
-        want_tiles = False  # the engine runs such grids on 64-token tiles (see _engine)
+        want_tiles = False  # the engine runs such grids on 64-token tiles (_as_64_token_grid)
     return ops.mask_from_lines(selected_lines, modes, n=n_video,
                                blocks_per_frame=max(int(blocks_per_frame), 1), layout=layout,
                                nb=nb, text_blocks=text_block_num, block_size=block_size,
@@ -255,6 +255,21 @@ def _kv_valid(pre_defined_mask: torch.Tensor) -> int:
     return int(pre_defined_mask[0].sum().item())
 
 
+def _as_64_token_grid(mask: torch.Tensor, seq_len: int, origin: int):
+    """(mask64, origin64) for a 128-token block mask on a grid starting `origin` in
+    [-127, -64] tokens before token 0.
+
+    The kernels run 64-key tiles on grids that start in (-64, 0]. This grid is the 64-token
+    grid 64 tokens later whose first tile row and column are all padding: each 128-block
+    row and column becomes two 64-token ones, the first of each is dropped, and the rest is
+    cut to the tiles the sequence reaches. Run with exact rows, every 64-row half keeps its
+    128-block row's mask, so the token-level mask is the same."""
+    origin64 = origin + 64
+    n64 = -(-(seq_len - origin64) // 64)
+    m64 = mask.repeat_interleave(2, dim=1).repeat_interleave(2, dim=2)
+    return m64[:, 1:n64 + 1, 1:n64 + 1], origin64
+
+
 def _engine(query, key, value, mask, tiles, pre_defined_mask, video_token_num, block_size,
             union_rows, grid_origin=0, precision="bf16"):
     if mask.dim() == 2:
@@ -262,15 +277,7 @@ def _engine(query, key, value, mask, tiles, pre_defined_mask, video_token_num, b
     q8 = precision == "int8"
     if pre_defined_mask is None:
         if block_size == 128 and grid_origin <= -64:
-            # The kernels run 64-key tiles on a grid that starts in (-64, 0]. A 128-block
-            # grid starting 64..127 tokens before token 0 is the 64-tile grid 64 tokens
-            # later with its first tile row and column all padding. Each 128-block row
-            # keeps its own mask on both of its 64-row halves (exact rows), so the token
-            # mask is the same.
-            grid_origin += 64
-            n64 = -(-(query.shape[2] - grid_origin) // 64)  # tiles the sequence reaches
-            m64 = mask.repeat_interleave(2, dim=1).repeat_interleave(2, dim=2)
-            m64 = m64[:, 1:n64 + 1, 1:n64 + 1]
+            m64, grid_origin = _as_64_token_grid(mask, query.shape[2], grid_origin)
             tiles = ops.mask_to_tiles(m64, 64, union_rows=False, grid_origin=grid_origin)
         elif tiles is None:
             tiles = ops.mask_to_tiles(mask, block_size, union_rows=union_rows,

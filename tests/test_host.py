@@ -274,3 +274,31 @@ def test_board_sampler_without_amdsmi_reports_none(monkeypatch):
     with bench.BoardSampler() as b:
         pass
     assert b.result() is None
+
+
+def test_64_token_grid_of_a_128_block_mask_realises_the_same_token_mask():
+    """attn_mask._as_64_token_grid: for random 128-token block masks on text-first grids
+    starting 64..127 tokens early, the exact-row 64-tile lists of the converted mask
+    realise the token mask of the original 128-block lists (oracle token masks)."""
+    from mod_dit_amd.attn_mask import _as_64_token_grid
+
+    rng = np.random.default_rng(5)
+    checked = 0
+    for _ in range(40):
+        text = int(rng.integers(1, 64)) + 128 * int(rng.integers(0, 3))  # text % 128 in 1..63
+        video = int(rng.integers(1, 900))
+        tb, vb, origin = O.cogvideox_grid(text, video, 128)
+        assert -127 <= origin <= -65
+        S = text + video
+        H = int(rng.integers(1, 3))
+        nb = tb + vb
+        m = rng.random((H, nb, nb)) < float(rng.uniform(0.1, 0.9))
+        _, lists = O.tiles_from_mask(m, 128, False)
+        want = O.token_mask_from_tiles(lists, H, S, S, origin=origin)
+        m64, origin64 = _as_64_token_grid(torch.from_numpy(m), S, origin)
+        assert -64 < origin64 <= 0 and m64.shape[1] == -(-(S - origin64) // 64)
+        _, lists64 = O.tiles_from_mask(m64.numpy(), 64, False)
+        got = O.token_mask_from_tiles(lists64, H, S, S, origin=origin64)
+        assert np.array_equal(got, want), (text, video)
+        checked += 1
+    assert checked == 40
