@@ -14,6 +14,8 @@ tile rows, mask density and, for text-first layouts, a shifted block grid. It ch
   blocks included), batches of 1-2;
 - the fused dense + map kernel against the separate replay of its own LSE (bit-exact)
   and fp64 attention;
+- the quantiser bit-exact on random shapes, grids and layouts; M^T S of fp32 maps within
+  the worst-case fp32 summation bound; the refresh merge on strided masks (bit-exact);
 - M^T S on arbitrary finite fp16 (bit-exact), the fit against the fp64 ridge solution
   (2e-6 of max|X|), and line selection with ties, signed zeros and NaN (bit-exact);
 - batches of 1-3 in both input layouts with strided outputs, and dense attention with
@@ -519,3 +521,68 @@ def test_random_batches_layouts_and_cross_lengths(i):
         ref, _ = O.masked_attention(_np(q[b]), _np(k2[b]), _np(v2[b]), tm, dtype=np.float64)
         err = np.abs(_np(out2[b]).astype(np.float64) - ref)
         assert err.max() <= 2e-2 and err.mean() <= 2e-3, (tag, "sparse", b, err.max())
+
+
+# ---------------------------------------------------------------- quantiser, fp32 M^T S, merge
+@pytest.mark.parametrize("i", range(8))
+def test_random_quantiser_bit_exact(i):
+    """The int8/fp8 quantiser on random shapes, grids, layouts and input offsets: every
+    quantised tensor and scale bit-exact to the oracle given the kernel's K mean."""
+    rng = np.random.default_rng(23000 + i)
+    H = int(rng.integers(1, 4))
+    S = int(rng.integers(1, 2000))
+    D = int(rng.choice([64, 128]))
+    dtype = [torch.bfloat16, torch.float16][int(rng.integers(0, 2))]
+    origin = -int(rng.integers(0, 64)) if rng.random() < 0.5 else 0
+    bshd = bool(rng.integers(0, 2))
+    tag = f"case {i}: H={H} S={S} D={D} {dtype} origin={origin} bshd={bshd}"
+    print(tag, flush=True)
+    g = torch.Generator().manual_seed(24000 + i)
+    shift = [float(rng.normal()) for _ in range(3)]
+    if bshd:
+        q, k, v = ((torch.randn((1, S, H, D), generator=g) * (1 + j) + shift[j])
+                   .to(dtype).to(DEV).transpose(1, 2) for j in range(3))
+    else:
+        q, k, v = ((torch.randn((1, H, S, D), generator=g) * (1 + j) + shift[j])
+                   .to(dtype).to(DEV) for j in range(3))
+    qz = ops.quantize_qkv(q, k, v, grid_origin=origin)
+    ref = O.quantize_qkv(_np(q[0]), _np(k[0]), _np(v[0]), k_mean=qz.k_mean[0].cpu().numpy(),
+                         origin=origin)
+    got = dict(q8=qz.q8[0].cpu().numpy(), q_scale=qz.q_scale[0].cpu().numpy(),
+               k8=qz.k8[0].cpu().numpy(), k_scale=qz.k_scale[0].cpu().numpy(),
+               v8t=qz.v8t[0].cpu().numpy(), v_scale=qz.v_scale[0].cpu().numpy())
+    for name in got:
+        assert got[name].shape == ref[name].shape and np.array_equal(got[name], ref[name]), \
+            (tag, name)
+    np.testing.assert_allclose(qz.k_mean[0].cpu().numpy(), _np(k[0]).astype(np.float64).mean(axis=1),
+                               rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("i", range(6))
+def test_random_mts_fp32_maps(i):
+    rng = np.random.default_rng(25000 + i)
+    n = int(rng.integers(2, 400))
+    bpf = int(rng.integers(1, max(2, n // 2)))
+    H = int(rng.integers(1, 4))
+    S32 = rng.normal(size=(H, n, n)).astype(np.float32)
+    got = md.compute_mts(torch.from_numpy(S32).to(DEV), bpf).cpu().numpy()
+    want = np.stack([O.moddit_ref._mts_f64(S32[h].astype(np.float64), bpf) for h in range(H)])
+    # worst case of an fp32 sum of m <= n*bpf terms in any order, plus the final rounding:
+    # (m + 1) * 2^-24 * (sum of |terms|) per output; the sum of |terms| is M^T |S|
+    mag = np.stack([O.moddit_ref._mts_f64(np.abs(S32[h]).astype(np.float64), bpf)
+                    for h in range(H)])
+    m = n * max(bpf, 1)
+    assert np.all(np.abs(got - want) <= (m + 1) * 2.0 ** -24 * mag + 1e-30), (n, bpf, H)
+
+
+@pytest.mark.parametrize("i", range(6))
+def test_random_refresh_merge_exact(i):
+    rng = np.random.default_rng(26000 + i)
+    H, n = int(rng.integers(1, 5)), int(rng.integers(1, 300))
+    pad = int(rng.integers(0, 9))
+    prev = rng.random((H, n, n)).astype(np.float16)
+    cur = rng.random((H, n, n)).astype(np.float16)
+    full = rng.random((H, n + pad, n + pad)) < float(rng.uniform(0.05, 0.95))
+    mask = torch.from_numpy(full).to(DEV)[:, :n, :n]  # a strided view when pad > 0
+    got = ops.refresh_merge(torch.from_numpy(prev).to(DEV), torch.from_numpy(cur).to(DEV), mask)
+    assert np.array_equal(got.cpu().numpy(), O.refresh_merge(prev, cur, full[:, :n, :n])), (H, n, pad)
