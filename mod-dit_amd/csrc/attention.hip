@@ -274,11 +274,15 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
     if constexpr (kRagged) {
       const int key0 = p.origin + kt * kBN;
       if (key0 < 0 || key0 + kBN > p.kv_len) {
+        // element i of s0 is key key0 + 8*half + c, c = 16*(i>>3) + (i&7) (s1: c + 32);
+        // comparing the constant c against per-tile bounds keeps no per-element value live
+        const int lo = -key0 - 8 * half;           // key >= 0       <=> c >= lo
+        const int hi = p.kv_len - key0 - 8 * half; // key < kv_len   <=> c < hi
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int k0 = key0 + (i >> 3) * 16 + 8 * half + (i & 7);
-          if (k0 < 0 || k0 >= p.kv_len) s0[i] = -INFINITY;
-          if (k0 + 32 < 0 || k0 + 32 >= p.kv_len) s1[i] = -INFINITY;
+          const int c = (i >> 3) * 16 + (i & 7);
+          if (c < lo || c >= hi) s0[i] = -INFINITY;
+          if (c + 32 < lo || c + 32 >= hi) s1[i] = -INFINITY;
         }
       }
     }

@@ -286,11 +286,14 @@ __global__ __launch_bounds__(kThreads, kRagged ? 2 : 3) __attribute__((amdgpu_wa
     } else {
       // keys outside [0, seq_len) are padding of the grid: masked
       const float sc = kscale[kt] * q_sc;
+      // element i of f0 is key key0 + 32*half + i (f1: + 16); comparing the constant i
+      // against per-tile bounds keeps no per-element value live across the loop
+      const int lo = -key0 - 32 * half;            // key >= 0       <=> i >= lo
+      const int hi = p.seq_len - key0 - 32 * half; // key < seq_len  <=> i < hi
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int k0 = key0 + 32 * half + i;
-        f0[i] = (k0 < 0 || k0 >= p.seq_len) ? -INFINITY : static_cast<float>(s0[i]) * sc;
-        f1[i] = (k0 + 16 < 0 || k0 + 16 >= p.seq_len) ? -INFINITY : static_cast<float>(s1[i]) * sc;
+        f0[i] = (i < lo || i >= hi) ? -INFINITY : static_cast<float>(s0[i]) * sc;
+        f1[i] = (i + 16 < lo || i + 16 >= hi) ? -INFINITY : static_cast<float>(s1[i]) * sc;
       }
       mx = f0[0];
 #pragma unroll
