@@ -78,7 +78,11 @@ int moddit_flash_fwd(const void* q, const void* k, const void* v, void* o, float
  * padding: such keys are masked out and such query rows are not written. A negative
  * origin lets text-first sequences whose text is not block-aligned (CogVideoX: 226 text
  * tokens) start both text and video on block boundaries without copying; the
- * reference rejects such shapes (MoD/mod/triton_flash_sparsity.py:157-160).
+ * reference rejects such shapes (MoD/mod/triton_flash_sparsity.py:157-160). A grid of
+ * 128-token blocks starting 64..127 tokens early is the 64-token grid 64 tokens later
+ * whose first tile row and column are padding: pass that grid, with rows kept per
+ * 64-row half. Entries naming a key tile outside [0, ceil((kv_len - grid_origin)/64))
+ * hold no keys and are skipped.
  * n_qtiles must equal ceil((q_len - grid_origin) / 128).
  * Replaces block_sparse_sage2_attn_cuda (MoD/mod/attn_mask.py:306,312-317) as driven
  * by AttentionSparseEngine (attn_mask.py:266-331).
