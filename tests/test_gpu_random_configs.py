@@ -7,7 +7,7 @@ tile rows, mask density and, for text-first layouts, a shifted block grid. It ch
   the north-star bound (max-abs <= 2e-2, mean-abs <= 2e-3) and an LSE bound of 2e-3;
 - the int8/fp8 block-sparse kernel against the oracle's model of its arithmetic (the
   bounds of tests/test_gpu_q8.py: 4e-3 max-abs, 3e-4 mean-abs, 2e-4 on the LSE; rare
-  e4m3 rounding-boundary elements up to 2e-2, see _check_q8_model);
+  rows with an e4m3 rounding-boundary flip up to 2e-2, see _check_q8_model);
 - masks and tile lists generated from selected lines, bit-exactly;
 - the replay map of exact (quarter-integer) scores against the oracle's replay of the
   same LSE, bit-exactly, for the wan, hunyuan and cogvideox layouts (partial last video
@@ -57,15 +57,16 @@ def _check_q8_model(err, tag):
     """The int8/fp8 kernel against the oracle's fp64 model of its arithmetic: 4e-3 max-abs
     and 3e-4 mean-abs (tests/test_gpu_q8.py), except where a weight P lies on an e4m3
     rounding boundary and the kernel (fp32 exp2) and the model (fp64) round it one code
-    apart: 2^-3 relative, which moves O by up to w |v| / 8 for a dominant weight w. Such
-    elements must be rare (at most 1e-5 of the output, at least one allowed) and stay
-    within 2e-2."""
-    n_over = int((err > 4e-3).sum())
+    apart: 2^-3 relative, which moves a row's outputs by up to w |v| / 8 for a dominant
+    weight w. Rows with such elements must be rare (at most 1e-3 of the rows, at least two
+    allowed) and every element stays within 2e-2."""
+    rows_over = int((err.max(axis=-1) > 4e-3).sum())
+    n_rows = err.size // err.shape[-1]
     print(f"  q8 vs model: max-abs {err.max():.3e} mean-abs {err.mean():.3e} "
-          f"above 4e-3: {n_over} of {err.size}", flush=True)
+          f"rows above 4e-3: {rows_over} of {n_rows}", flush=True)
     assert err.mean() <= 3e-4, (tag, err.mean())
     assert err.max() <= 2e-2, (tag, err.max())
-    assert n_over <= max(1, int(1e-5 * err.size)), (tag, n_over)
+    assert rows_over <= max(2, int(1e-3 * n_rows)), (tag, rows_over)
 
 
 def _draw_attention(i):
@@ -325,14 +326,9 @@ def test_random_select_lines_bit_exact(i):
 
 
 # ---------------------------------------------------------------- whole schedules
-@pytest.mark.parametrize("i", range(16))
-def test_random_schedule_sparse_steps(i):
-    """SparseAttentionWithMap over W-2 .. W+T+1 (map, fit, predict, sparse, refresh,
-    sparse) on a random wan or text-first cogvideox layer. Every sparse step's output is
-    checked against fp64 attention (bf16) or the oracle's model of the quantised
-    arithmetic (int8) under the mask the state holds, as the kernels execute it; every
-    map step's output against fp64 dense attention."""
-    rng = np.random.default_rng(16000 + i)
+def _schedule_wan_cogvideox(i, seed, vary_dtype_and_threshold=False):
+    """One random wan / text-first cogvideox schedule (see the tests below)."""
+    rng = np.random.default_rng(seed + i)
     model_type = ["wan", "cogvideox"][int(rng.integers(0, 2))]
     bs = int(rng.choice([64, 128]))
     tile_rows = ["exact", "union"][int(rng.integers(0, 2))]
@@ -349,19 +345,23 @@ def test_random_schedule_sparse_steps(i):
     W, T = int(rng.integers(3, 6)), int(rng.integers(2, 4))
     n_v = -(-video // bs)
     top_k = int(rng.integers(1, max(2, 3 * n_v // 2)))
+    dtype, thr = torch.bfloat16, 1e-3
+    if vary_dtype_and_threshold:
+        dtype = [torch.bfloat16, torch.float16][int(rng.integers(0, 2))]
+        thr = float(10.0 ** rng.uniform(-4.5, -1.5))
     origin = O.cogvideox_grid(text, video, bs)[2] if model_type == "cogvideox" else 0
     tag = (f"case {i}: {model_type} bs={bs} {tile_rows} {precision} H={H} D={D} F={F} "
-           f"tpf={tpf} text={text} W={W} T={T} top_k={top_k}")
+           f"tpf={tpf} text={text} W={W} T={T} top_k={top_k} {dtype} thr={thr:.2e}")
     print(tag, flush=True)
     st = md.create_adaptive_mask_state(model_type, H, video, text, tpf, F, warmup_steps=W,
-                                       top_k=top_k, predict_T=T, threshold=1e-3,
+                                       top_k=top_k, predict_T=T, threshold=thr,
                                        block_size=bs, tile_rows=tile_rows, precision=precision)
-    base = [torch.randn(1, H, S, D, generator=torch.Generator().manual_seed(17000 + 10 * i + j))
+    base = [torch.randn(1, H, S, D, generator=torch.Generator().manual_seed(seed + 1000 + 10 * i + j))
             for j in range(3)]
     checked = 0
     for step in range(W - 2, W + T + 2):
-        g = torch.Generator().manual_seed(18000 + 100 * i + step)
-        q, k, v = ((b + 0.3 * torch.randn(b.shape, generator=g)).to(torch.bfloat16).to(DEV)
+        g = torch.Generator().manual_seed(seed + 2000 + 100 * i + step)
+        q, k, v = ((b + 0.3 * torch.randn(b.shape, generator=g)).to(dtype).to(DEV)
                    for b in base)
         phase = O.step_phase(step, W, T)
         out, _ = md.SparseAttentionWithMap(q, k, v, st, None, current_step=step)
@@ -394,6 +394,23 @@ def test_random_schedule_sparse_steps(i):
               flush=True)
         checked += 1
     assert checked >= 2, tag
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_random_schedule_sparse_steps(i):
+    """SparseAttentionWithMap over W-2 .. W+T+1 (map, fit, predict, sparse, refresh,
+    sparse) on a random wan or text-first cogvideox layer in bf16 at threshold 1e-3.
+    Every sparse step's output is checked against fp64 attention (bf16) or the oracle's
+    model of the quantised arithmetic (int8) under the mask the state holds, as the
+    kernels execute it; every map step's output against fp64 dense attention."""
+    _schedule_wan_cogvideox(i, 16000)
+
+
+@pytest.mark.parametrize("i", range(10))
+def test_random_schedule_fp16_inputs_and_thresholds(i):
+    """As above with bf16 or fp16 inputs (the reference runs CogVideoX in fp16) and map
+    thresholds drawn from 3e-5 .. 3e-2."""
+    _schedule_wan_cogvideox(i, 27000, vary_dtype_and_threshold=True)
 
 
 @pytest.mark.parametrize("i", range(10))
