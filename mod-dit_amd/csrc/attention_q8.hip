@@ -256,7 +256,9 @@ __global__ __launch_bounds__(kThreads, kRagged ? 2 : 3) __attribute__((amdgpu_wa
     float f0[16], f1[16];
     float mx;
     bool general = false;
-    if constexpr (kRagged) general = key0 < 0 || key0 + kBN > p.seq_len || p.origin != 0;
+    // tiles wholly inside the sequence share one K scale on any grid (the quantiser's
+    // blocks lie on the attention grid), so only tiles that cross 0 or seq_len need masking
+    if constexpr (kRagged) general = key0 < 0 || key0 + kBN > p.seq_len;
     if (!general) {
       // whole tile inside the sequence, one quantisation tile: max over the raw scores
       const float sc = kscale[kt] * q_sc;
