@@ -9,8 +9,9 @@
 // A tile is D bytes per key for K and for V, so a 3-stage ring takes 48 KB of LDS at
 // D=128: K tiles are fetched three tiles ahead, V tiles two, each into the stage its
 // predecessor three tiles back left free at the previous barrier. 48 KB and 166 VGPRs
-// let three workgroups share a CU (three waves per SIMD) in the aligned kernel; the
-// ragged kernel needs 234 VGPRs and runs two.
+// let three workgroups share a CU (three waves per SIMD) in the aligned kernel. The
+// ragged kernels convert the scores once and mask boundary tiles in place: 139 VGPRs at
+// D=64 (three waves), 199 at D=128 (two; three would spill).
 //
 // Operand layouts. MFMA products are sums over k, so any assignment of (lane half, byte)
 // to k works as long as both operands use the same one; the layouts below are chosen so
@@ -94,7 +95,7 @@ __device__ __forceinline__ int swz_k8(int r) { return (r / (256 / D)) % (D / 16)
 __device__ __forceinline__ int swz_v8(int r) { return (r >> 2) & 3; }
 
 template <int D, typename E, bool kSparse, bool kRagged>
-__global__ __launch_bounds__(kThreads, kRagged ? 2 : 3) __attribute__((amdgpu_waves_per_eu(kRagged ? 2 : 3, kRagged ? 2 : 3))) void attention_q8_kernel(Q8Params p) {
+__global__ __launch_bounds__(kThreads, (kRagged && D == 128) ? 2 : 3) __attribute__((amdgpu_waves_per_eu((kRagged && D == 128) ? 2 : 3, (kRagged && D == 128) ? 2 : 3))) void attention_q8_kernel(Q8Params p) {
   using L = Q8Lds<D>;
   constexpr int kKSteps = D / 32;                // int8 MFMA k-steps over d
   constexpr int kDSub = D / 32;                  // 32-row blocks of O^T
@@ -259,9 +260,9 @@ __global__ __launch_bounds__(kThreads, kRagged ? 2 : 3) __attribute__((amdgpu_wa
     // tiles wholly inside the sequence share one K scale on any grid (the quantiser's
     // blocks lie on the attention grid), so only tiles that cross 0 or seq_len need masking
     if constexpr (kRagged) general = key0 < 0 || key0 + kBN > p.seq_len;
-    if (!general) {
-      // whole tile inside the sequence, one quantisation tile: max over the raw scores
-      const float sc = kscale[kt] * q_sc;
+    const float sc = kscale[kt] * q_sc;  // one K scale per tile on any grid, q_sc > 0
+    if constexpr (!kRagged) {
+      // every tile inside the sequence: max over the raw integer scores
       int mi = s0[0];
 #pragma unroll
       for (int i = 1; i < 16; ++i) mi = max(mi, s0[i]);
@@ -286,22 +287,39 @@ __global__ __launch_bounds__(kThreads, kRagged ? 2 : 3) __attribute__((amdgpu_wa
         f1[i] = __builtin_fmaf(f1[i], sc, -m_sh);
       }
     } else {
-      // keys outside [0, seq_len) are padding of the grid: masked
-      const float sc = kscale[kt] * q_sc;
-      // element i of f0 is key key0 + 32*half + i (f1: + 16); comparing the constant i
-      // against per-tile bounds keeps no per-element value live across the loop
-      const int lo = -key0 - 32 * half;            // key >= 0       <=> i >= lo
-      const int hi = p.seq_len - key0 - 32 * half; // key < seq_len  <=> i < hi
+      // ragged grids: the scores are converted once and, on tiles that cross 0 or
+      // seq_len, masked in place, so both paths share the same registers
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        f0[i] = (i < lo || i >= hi) ? -INFINITY : static_cast<float>(s0[i]) * sc;
-        f1[i] = (i + 16 < lo || i + 16 >= hi) ? -INFINITY : static_cast<float>(s1[i]) * sc;
+        f0[i] = static_cast<float>(s0[i]);
+        f1[i] = static_cast<float>(s1[i]);
       }
-      mx = f0[0];
+      if (general) {
+        // keys outside [0, seq_len) are padding of the grid: masked in place. Element i of
+        // f0 is key key0 + 32*half + i (f1: + 16); comparing the constant i with per-tile
+        // bounds keeps no per-element value live across the loop.
+        const int lo = -key0 - 32 * half;            // key >= 0       <=> i >= lo
+        const int hi = p.seq_len - key0 - 32 * half; // key < seq_len  <=> i < hi
 #pragma unroll
-      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, f0[i]);
+        for (int i = 0; i < 16; ++i) {
+          if (i < lo || i >= hi) f0[i] = -INFINITY;
+          if (i + 16 < lo || i + 16 >= hi) f1[i] = -INFINITY;
+        }
+        float mr = f0[0];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, f1[i]);
+        for (int i = 1; i < 16; ++i) mr = fmaxf(mr, f0[i]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mr = fmaxf(mr, f1[i]);
+        mx = mr * sc;
+      } else {
+        // whole tile inside the sequence: max over the raw integer scores
+        int mi = s0[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) mi = max(mi, s0[i]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mi = max(mi, s1[i]);
+        mx = static_cast<float>(mi) * sc;
+      }
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const bool need = mx > m_run + kRescaleSlack;
       rescale = __ballot(need) != 0ull;
@@ -309,11 +327,12 @@ __global__ __launch_bounds__(kThreads, kRagged ? 2 : 3) __attribute__((amdgpu_wa
       // exp2(0) = 1 when the max is kept; fminf drops the NaN of -inf - -inf
       alpha = __builtin_amdgcn_exp2f(__builtin_fminf(m_run - m_new, 0.f));
       m_run = m_new;
+      // a row whose keys so far are all masked keeps m = -inf: shift by 0 (P = 0 anyway)
       const float m_sh = ((m_new == -INFINITY) ? 0.f : m_new) - kPShift;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        f0[i] -= m_sh;
-        f1[i] -= m_sh;
+      for (int i = 0; i < 16; ++i) {  // -inf * sc - m_sh stays -inf (sc > 0)
+        f0[i] = __builtin_fmaf(f0[i], sc, -m_sh);
+        f1[i] = __builtin_fmaf(f1[i], sc, -m_sh);
       }
     }
     float rs = 0.f;
