@@ -164,12 +164,20 @@ def measured_traffic(name="attention_hunyuan_headline.md"):
     return None, None
 
 
+def best_ceiling(kinds):
+    """The highest sustained rate over MFMA shapes of one data type (each shape measured
+    by mfma_ceiling), and every shape's row."""
+    rows = [r for r in (mfma_ceiling(k) for k in kinds) if r is not None]
+    return (max(rows, key=lambda r: r["value"]) if rows else None), rows
+
+
 def mfma_ceiling(kind, iters=4000, reps=200, zeros=False):
     """MFMA rate and shader clock on random operands, from the calibration library built
     next to libmoddit.so (mod-dit_amd/csrc/calib/mfma_ceiling.hip): back-to-back MFMAs
     only, two waves per SIMD, one 8-wave workgroup per CU. kind 0: bf16 32x32x16, 1: int8
-    32x32x32, 2: fp8 e4m3 32x32x64. Under sustained MFMA load the clock settles at the
-    board's power limit, so this is the rate the published peak shrinks to on real data.
+    32x32x32, 2: fp8 e4m3 32x32x64; 3-5: bf16 16x16x32, int8 16x16x64, fp8 16x16x128.
+    Under sustained MFMA load the clock settles at the board's power limit, so this is the
+    rate the published peak shrinks to on real data; the 16x16 shapes hold a higher clock.
     `zeros` runs the same loop on all-zero operands (for contrast: those draw less power).
     Returns None when the library is missing or the measurement fails."""
     path = os.path.join(ROOT, "mod-dit_amd", "libmoddit_calib.so")
@@ -184,8 +192,9 @@ def mfma_ceiling(kind, iters=4000, reps=200, zeros=False):
     if fn(kind, int(zeros), iters, reps, ctypes.byref(rate), ctypes.byref(mhz), ctypes.byref(cyc)) != 0:
         return None
     names = ("v_mfma_f32_32x32x16_bf16", "v_mfma_i32_32x32x32_i8",
-             "v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3)")
-    return {"value": round(rate.value, 1), "unit": "TOP/s" if kind == 1 else "TFLOP/s",
+             "v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3)", "v_mfma_f32_16x16x32_bf16",
+             "v_mfma_i32_16x16x64_i8", "v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3)")
+    return {"value": round(rate.value, 1), "unit": "TOP/s" if kind in (1, 4) else "TFLOP/s",
             "clock_mhz": round(mhz.value), "cycles_per_mfma_per_simd": round(cyc.value, 2),
             "mfma": names[kind], "operands": "zeros" if zeros else "random"}
 
@@ -738,11 +747,11 @@ def main(argv=None):
 
     if args.calibrate:
         rows = []
-        for kind in (0, 1, 2):
+        for kind in (0, 3, 1, 4, 2, 5):
             for z in (False, True):
                 # one call of ~800 back-to-back launches (~4 s): no gaps under the sampler
                 with BoardSampler() as board:
-                    row = mfma_ceiling(kind, reps=800 if kind != 2 else 400, zeros=z)
+                    row = mfma_ceiling(kind, reps=400 if kind in (2, 5) else 800, zeros=z)
                 if row is not None:
                     row["board"] = board.result()
                 rows.append(row)
@@ -937,9 +946,11 @@ def main(argv=None):
                            what=f"the {args.config}-like layer")
 
     log("measuring the MFMA ceiling on random operands")
-    ceiling = mfma_ceiling(0)
+    # the best bf16 rate the part sustains on data: 32x32x16 (the kernels' shape) or
+    # 16x16x32, whichever the board clocks higher
+    ceiling, ceiling_rows = best_ceiling((0, 3))
     if q8 is not None:
-        c8, cf8 = mfma_ceiling(1), mfma_ceiling(2)
+        (c8, _), (cf8, _) = best_ceiling((1, 4)), best_ceiling((2, 5))
         q8["mfma_ceiling_int8"], q8["mfma_ceiling_fp8"] = c8, cf8
         if c8 and cf8:
             # Q.K^T (int8) and P.V (fp8) each carry half of the executed operations
@@ -1002,6 +1013,7 @@ def main(argv=None):
             "kernel": "attention_fwd_kernel<128, Bf16, sparse>",
             "kernel_ms": round(kernel_ms, 4),
             "mfma_ceiling": ceiling,
+            "mfma_ceiling_by_shape": ceiling_rows,
             "frac_of_mfma_ceiling": (round(achieved / ceiling["value"], 4) if ceiling else None),
             "board": board,
             # the fraction of the bf16 MFMA peak computed from the measured clock: the same

@@ -7,11 +7,13 @@ import bench
 
 pytestmark = pytest.mark.gpu
 
-# kind -> (published dense peak at the top clock, ops per MFMA)
-PEAK = {0: (2500.0, 32768), 1: (5000.0, 65536), 2: (5000.0, 131072)}
+# kind -> (published dense peak at the top clock, ops per MFMA): the 32x32 shapes the
+# kernels use and the 16x16 shapes of the same types
+PEAK = {0: (2500.0, 32768), 1: (5000.0, 65536), 2: (5000.0, 131072),
+        3: (2500.0, 16384), 4: (5000.0, 32768), 5: (5000.0, 65536)}
 
 
-@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("kind", [0, 1, 2, 3, 4, 5])
 def test_mfma_ceiling_is_consistent(kind):
     r = bench.mfma_ceiling(kind, iters=400, reps=2)
     assert r is not None, "libmoddit_calib.so missing or the measurement failed"

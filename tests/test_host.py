@@ -43,7 +43,8 @@ def test_calibration_library_stays_outside_the_c_abi():
     fn.restype = ctypes.c_int
     d = ctypes.c_double()
     # argument errors are reported before any HIP call
-    assert fn(3, 0, 10, 1, ctypes.byref(d), ctypes.byref(d), ctypes.byref(d)) == 2
+    assert fn(6, 0, 10, 1, ctypes.byref(d), ctypes.byref(d), ctypes.byref(d)) == 2
+    assert fn(-1, 0, 10, 1, ctypes.byref(d), ctypes.byref(d), ctypes.byref(d)) == 2
     assert fn(0, 0, 0, 1, ctypes.byref(d), ctypes.byref(d), ctypes.byref(d)) == 2
     assert fn(0, 0, 10, 1, None, ctypes.byref(d), ctypes.byref(d)) == 2
 
