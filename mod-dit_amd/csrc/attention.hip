@@ -291,7 +291,7 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
     for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s0[i]);
 #pragma unroll
     for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s1[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = max_over_halves(mx);
     const float mxs = mx * p.scale_log2;
     const bool need = mxs > m_run + kRescaleSlack;
     rescale = __ballot(need) != 0ull;
@@ -394,7 +394,7 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(2, 
   }
 
   // ---- epilogue ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = sum_over_halves(l_run);
   if (q_row >= 0 && q_row < p.q_len) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + q_row * p.o_ss;

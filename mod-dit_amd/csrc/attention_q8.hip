@@ -274,7 +274,7 @@ __global__ __launch_bounds__(kThreads, (kRagged && D == 128) ? 2 : 3) __attribut
         f0[i] = static_cast<float>(s0[i]);
         f1[i] = static_cast<float>(s1[i]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = max_over_halves(mx);
       const bool need = mx > m_run + kRescaleSlack;
       rescale = __ballot(need) != 0ull;
       const float m_new = need ? mx : m_run;
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(kThreads, (kRagged && D == 128) ? 2 : 3) __attribut
         for (int i = 0; i < 16; ++i) mi = max(mi, s1[i]);
         mx = static_cast<float>(mi) * sc;
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = max_over_halves(mx);
       const bool need = mx > m_run + kRescaleSlack;
       rescale = __ballot(need) != 0ull;
       const float m_new = need ? mx : m_run;
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(kThreads, (kRagged && D == 128) ? 2 : 3) __attribut
   }
 
   // ---- epilogue: O = O^T * v_scale[d] / l ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = sum_over_halves(l_run);
   if (q_row >= 0 && q_row < p.q_len) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const float* vsc = p.v_scale + static_cast<int64_t>(bh) * D;

@@ -115,6 +115,18 @@ struct Fp16 {
   }
 };
 
+// Max / sum of x over lanes l and l ^ 32, in both lanes. v_permlane32_swap exchanges
+// the two 32-lane halves of a register pair in the VALU (no LDS round trip, unlike the
+// ds_bpermute behind __shfl_xor); both lanes of a pair get bit-identical results.
+__device__ __forceinline__ float max_over_halves(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+__device__ __forceinline__ float sum_over_halves(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+
 template <typename V>
 __device__ __forceinline__ V as_vec8(u32x4 x) {
   return __builtin_bit_cast(V, x);
