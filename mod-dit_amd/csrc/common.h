@@ -84,6 +84,9 @@ struct Bf16 {
   static __device__ __forceinline__ f32x16 mma(vec8 a, vec8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
+  static __device__ __forceinline__ f32x4 mma16(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
   static __device__ __forceinline__ float to_float(uint16_t u) {
     return __uint_as_float(static_cast<uint32_t>(u) << 16);
   }
@@ -101,6 +104,9 @@ struct Fp16 {
   typedef _Float16 elem;
   static __device__ __forceinline__ f32x16 mma(vec8 a, vec8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ float to_float(uint16_t u) {
     _Float16 h;

@@ -1,13 +1,20 @@
 // Replayed block sparsity map for gfx950.
 //
 // For each (batch*head, 128-row query tile of the video region) one workgroup of four
-// wave64s sweeps every 64-key tile of the video region:
-//   S^T (64 keys x 32 queries) = K . round(Q*scale)^T    bf16/fp16 MFMA 32x32x16, fp32
-// and counts the scores strictly below lse[row] + log_threshold. Each comparison is a
-// wave-wide ballot whose popcount lands in a scalar register, so the count per
-// (wave, key tile) needs no vector reduction. Counts are staged in LDS and combined
-// into (query block, key block) cells of 64x64 or 128x128 tokens, then written as
-// fp16(count / block_size^2).
+// wave64s sweeps every 64-key tile of the video region. Each wave owns 32 query rows as
+// two 16-row blocks and computes, on bf16/fp16 MFMA 16x16x32 with fp32 accumulation,
+//   S^T (16 keys x 16 queries) = K . round(Q*scale)^T   for 4 key blocks x 2 query blocks
+// (lane l: query 16qq + l%16, keys 16kb + 4(l/16) + j), and counts the scores strictly
+// below lse[row] + log_threshold. Each comparison is a wave-wide ballot whose popcount
+// lands in a scalar register, so the count per (wave, key tile) needs no vector
+// reduction. Counts are staged in LDS and combined into (query block, key block) cells
+// of 64x64 or 128x128 tokens, then written as fp16(count / block_size^2).
+//
+// K tiles go straight from HBM into LDS (buffer_load ... lds, no register staging) in an
+// XOR-swizzled row-major layout, double-buffered, one barrier per tile. Under the
+// board's power limit the 16x16 shape holds a higher clock than 32x32x16, and without
+// register staging it needs no more cycles. Its maps match the 32x32x16 form's
+// bit for bit on the tested layers (both accumulate the same products in fp32).
 //
 // Reference semantics: flash_sparsity_replay_kernel
 // (MoD/mod/cuda_flash_sparsity_kernel.cu:41-169): Q scaled in fp32 and rounded to the
@@ -15,6 +22,7 @@
 // __float2half_rn of count / block_size^2 (:158-163). The last video block may run past
 // the sequence end; rows and keys at or beyond seq_len are then not counted.
 #include "common.h"
+#include "lds_dma.h"
 
 namespace moddit {
 namespace {
@@ -26,11 +34,17 @@ constexpr int kFlush = 64;  // key tiles per flush; the LDS count ring holds two
 
 template <int D>
 struct ReplayLds {
-  static constexpr int kPitchK = D * 2 + 16;
-  static constexpr int kKBytes = kBN * kPitchK;
-  static constexpr int kCounts = 4 * 2 * kFlush * 4;  // int per (wave, ring slot)
+  static constexpr int kRowBytes = D * 2;              // one key row, no padding
+  static constexpr int kKBytes = kBN * kRowBytes;      // one 64-key K tile
+  static constexpr int kRowsPerWindow = 1024 / kRowBytes;
+  static constexpr int kWindows = kKBytes / 1024;      // 1 KB DMA windows per tile
+  static constexpr int kCounts = 4 * 2 * kFlush * 4;   // int per (wave, ring slot)
   static constexpr int kTotal = 2 * kKBytes + kCounts;
 };
+// 16-byte chunk swizzle of a K row (XOR on the chunk index): the 16 rows a 16-lane group
+// reads at one logical chunk land in distinct bank groups.
+template <int D>
+__device__ __forceinline__ int replay_swz(int r) { return (r / (128 / D)) % (D / 8); }
 
 struct ReplayParams {
   const uint16_t* q;
@@ -59,9 +73,6 @@ template <int D, typename E, bool kRagged>
 __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p) {
   using L = ReplayLds<D>;
   using V8 = typename E::vec8;
-  constexpr int kDChunks = D / 16;
-  constexpr int kVecPerRow = D / 8;
-  constexpr int kKVecs = kBN * kVecPerRow / kThreads;
 
   extern __shared__ __align__(16) unsigned char smem[];
   int* cnt = reinterpret_cast<int*>(smem + 2 * L::kKBytes);
@@ -69,8 +80,8 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int half = lane >> 5;
-  const int c32 = lane & 31;
+  const int c16 = lane & 15;
+  const int g = lane >> 4;
 
   const int tile = xcd_remap(blockIdx.x, gridDim.x, p.xcd_run);
   const int qt = tile % p.n_qtiles;
@@ -85,61 +96,70 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
   const int video_rows = p.nblk * p.block;
   const int vrow0 = qt * kBM + wave * 32;
   const bool wave_active = vrow0 < video_rows;  // blocks are multiples of 32 rows
-  const int vrow = vrow0 + c32;
+  constexpr int kDC = D / 32;
 
-  V8 qf[kDChunks];
-  float thr = -INFINITY;
-  {
+  // qf[qq][dc]: query row vrow0 + 16qq + c16, dims 32dc + 8g .. +7 (B operand of the
+  // 16x16x32 MFMA), rounded as bf16(q * scale) like the reference
+  V8 qf[2][kDC];
+  float thr[2];
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq) {
+    const int vrow = vrow0 + 16 * qq + c16;
     const bool row_ok = wave_active && vrow < p.valid_q;
     const int r = p.q_off + (row_ok ? vrow : 0);
     const u32x4* src = reinterpret_cast<const u32x4*>(qb + r * p.q_ss);
 #pragma unroll
-    for (int c = 0; c < kDChunks; ++c) {
-      const u32x4 raw = src[2 * c + half];
+    for (int c = 0; c < kDC; ++c) {
+      const u32x4 raw = src[4 * c + g];
       uint16_t e[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) e[j] = E::from_float(E::to_float(u16_at(raw, j)) * p.scale);
       const u32x4 packed = {pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]),
                             pack2(e[6], e[7])};
-      qf[c] = as_vec8<V8>(packed);
+      qf[qq][c] = as_vec8<V8>(packed);
     }
     // rows past the sequence end count nothing (no score is below -inf)
-    thr = row_ok ? p.lse[static_cast<int64_t>(bh) * p.seq_len + r] + p.log_thr : -INFINITY;
-    // Retire these loads before the loop (see attention.hip).
-    __builtin_amdgcn_s_waitcnt(0);
+    thr[qq] = row_ok ? p.lse[static_cast<int64_t>(bh) * p.seq_len + r] + p.log_thr : -INFINITY;
   }
+  // Retire these loads before the loop (see attention.hip).
+  __builtin_amdgcn_s_waitcnt(0);
 
-  // K rows of the video region through a buffer resource (loop-invariant VGPR offsets,
-  // tile offset in the SGPR offset when every tile is a full in-range tile; otherwise in
-  // the range-checked VGPR offset, so rows past the last key load zeros).
-  const int k_col = tid % kVecPerRow;
-  const int k_row0 = tid / kVecPerRow;
-  constexpr int kKRowStep = kThreads / kVecPerRow;
+  // K tiles go straight from HBM to LDS (buffer_load ... lds): window w of a stage holds
+  // rows [w*kRowsPerWindow, ...), lane l at byte l*16, each lane loading the logical
+  // chunk its physical position holds under the swizzle. Ragged grids keep the tile
+  // offset in the range-checked VGPR offset, so rows past the last key load zeros.
+  constexpr int kWinPerWave = L::kWindows / 4;
   const uint16_t* kvid = kb + static_cast<int64_t>(p.k_off) * p.k_ss;
-  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kvid, p.k_bytes);
-  const uint32_t k_voff = static_cast<uint32_t>((k_row0 * p.k_ss + k_col * 8) * 2);
-  const uint32_t k_row_step = static_cast<uint32_t>(kKRowStep * p.k_ss * 2);
-  const uint32_t k_tile_bytes = static_cast<uint32_t>(kBN * p.k_ss * 2);
-  u32x4 kreg[kKVecs];
-  auto load_tile = [&](int kt) {
-    const uint32_t so = static_cast<uint32_t>(kt) * k_tile_bytes;
+  const u32x4 k_rsrc = raw_rsrc(kvid, p.k_bytes);
+  const uint32_t k_lds = lds_addr(smem);
+  uint32_t k_src[kWinPerWave];
 #pragma unroll
-    for (int i = 0; i < kKVecs; ++i) {
+  for (int i = 0; i < kWinPerWave; ++i) {
+    const int w = wave * kWinPerWave + i;
+    const int r = w * L::kRowsPerWindow + (lane * 16) / L::kRowBytes;
+    const int pch = ((lane * 16) % L::kRowBytes) / 16;
+    k_src[i] = static_cast<uint32_t>((r * p.k_ss + (pch ^ replay_swz<D>(r)) * 8) * 2);
+  }
+  const uint32_t k_tile_bytes = static_cast<uint32_t>(kBN * p.k_ss * 2);
+  auto dma_tile = [&](int kt, int stage) {
+    const uint32_t to = static_cast<uint32_t>(kt) * k_tile_bytes;
+#pragma unroll
+    for (int i = 0; i < kWinPerWave; ++i) {
+      const uint32_t dst = k_lds + stage * L::kKBytes + (wave * kWinPerWave + i) * 1024;
       if constexpr (kRagged)
-        kreg[i] = buf_load16(k_rsrc, k_voff + so + i * k_row_step, 0);
+        lds_dma16(k_rsrc, dst, k_src[i] + to, 0);
       else
-        kreg[i] = buf_load16(k_rsrc, k_voff, so + i * k_row_step);
+        lds_dma16(k_rsrc, dst, k_src[i], to);
     }
   };
-  auto store_tile = [&](int stage) {
-    unsigned char* ks = smem + stage * L::kKBytes;
+  // K (A operand): row 16kb + c16, logical chunk 4dc + g; the swizzle depends on c16 only
+  uint32_t k_rd[kDC];
 #pragma unroll
-    for (int i = 0; i < kKVecs; ++i)
-      *reinterpret_cast<u32x4*>(ks + (k_row0 + i * kKRowStep) * L::kPitchK + k_col * 16) = kreg[i];
-  };
+  for (int c = 0; c < kDC; ++c)
+    k_rd[c] = static_cast<uint32_t>(c16 * L::kRowBytes + (((4 * c + g) ^ replay_swz<D>(c16)) * 16));
 
-  load_tile(0);
-  store_tile(0);
+  dma_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   const float inv_area = 1.0f / static_cast<float>(p.block * p.block);
@@ -147,43 +167,52 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
 
   for (int it = 0; it < p.n_ktiles; ++it) {
     const bool has_next = it + 1 < p.n_ktiles;
-    if (has_next) load_tile(it + 1);
+    // the stage of tile it+1 held tile it-1, which every wave finished reading before
+    // the previous iteration's barrier
+    if (has_next) dma_tile(it + 1, (it + 1) & 1);
 
     if (wave_active) {
       const unsigned char* ks = smem + (it & 1) * L::kKBytes;
-      f32x16 s0 = f32x16{};
-      f32x16 s1 = f32x16{};
+      // s[kb][qq]: keys 16kb + 4g + j of query vrow0 + 16qq + c16
+      f32x4 s[4][2];
 #pragma unroll
-      for (int c = 0; c < kDChunks; ++c) {
-        const V8 a0 = *reinterpret_cast<const V8*>(ks + c32 * L::kPitchK + c * 32 + half * 16);
-        const V8 a1 =
-            *reinterpret_cast<const V8*>(ks + (32 + c32) * L::kPitchK + c * 32 + half * 16);
-        s0 = E::mma(a0, qf[c], s0);
-        s1 = E::mma(a1, qf[c], s1);
+      for (int kb = 0; kb < 4; ++kb) s[kb][0] = s[kb][1] = f32x4{};
+#pragma unroll
+      for (int c = 0; c < kDC; ++c) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const V8 a = *reinterpret_cast<const V8*>(ks + k_rd[c] + 16 * kb * L::kRowBytes);
+          s[kb][0] = E::mma16(a, qf[0][c], s[kb][0]);
+          s[kb][1] = E::mma16(a, qf[1][c], s[kb][1]);
+        }
       }
       int total = 0;
       if (kRagged && it * kBN + kBN > p.valid_k) {
         // keys at or past the sequence end are not counted
-        const int key0 = it * kBN + 4 * half;
+        const int key0 = it * kBN + 4 * g;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kr = key0 + 8 * (i >> 2) + (i & 3);
-          total += __builtin_popcountll(__ballot(s0[i] < thr && kr < p.valid_k));
-          total += __builtin_popcountll(__ballot(s1[i] < thr && kr + 32 < p.valid_k));
-        }
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bool kin = key0 + 16 * kb + j < p.valid_k;
+            total += __builtin_popcountll(__ballot(s[kb][0][j] < thr[0] && kin));
+            total += __builtin_popcountll(__ballot(s[kb][1][j] < thr[1] && kin));
+          }
       } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          total += __builtin_popcountll(__ballot(s0[i] < thr));
-          total += __builtin_popcountll(__ballot(s1[i] < thr));
-        }
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            total += __builtin_popcountll(__ballot(s[kb][0][j] < thr[0]));
+            total += __builtin_popcountll(__ballot(s[kb][1][j] < thr[1]));
+          }
       }
       // two halves of kFlush slots: a flush reads one half while the next kFlush key
       // tiles (at least one barrier later) write the other
       if (lane == 0) cnt[wave * 2 * kFlush + (it % (2 * kFlush))] = total;
     }
 
-    if (has_next) store_tile((it + 1) & 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     const int slot_hi = it % kFlush;
