@@ -330,13 +330,33 @@ def AttentionSparseEngine(query, key, value, mask, pre_defined_mask=None, video_
                    block_size, union_rows, precision=precision)
 
 
-def _dense_engine(query, key, value, pre_defined_mask):
-    """All-True mask: every query attends to the valid keys (MoD/mod/attn_mask.py:268-295;
-    the reference's video/text split there is the same computation)."""
-    if pre_defined_mask is not None:
-        kv = _kv_valid(pre_defined_mask)
-        key, value = key[:, :, :kv], value[:, :, :kv]
-    out, _ = ops.flash_fwd(query, key, value, return_lse=False)
+def _dense_engine(query, key, value, pre_defined_mask, video_token_num=0, precision="bf16"):
+    """All-True mask: every query attends to the valid keys (MoD/mod/attn_mask.py:268-295).
+
+    bf16: one dense call (the reference's video/text split there is the same computation).
+    int8: the video queries run the int8/fp8 kernels over the valid keys, as the
+    reference's sageattn call does (:271-276, K smoothed by the mean of those keys); the
+    text queries of a padded layout stay bf16, as its flashinfer call is (:278-290).
+    """
+    kv = key.shape[2] if pre_defined_mask is None else _kv_valid(pre_defined_mask)
+    if precision != "int8":
+        out, _ = ops.flash_fwd(query, key[:, :, :kv], value[:, :, :kv], return_lse=False)
+        return out
+    if pre_defined_mask is None:
+        out, _ = ops.flash_fwd_q8(ops.quantize_qkv(query, key, value), return_lse=False)
+        return out
+    S = query.shape[2]
+    video = int(video_token_num)
+    if not 0 <= video <= kv:
+        raise ValueError(f"video_token_num={video} must lie in [0, valid keys={kv}]")
+    out = torch.empty_like(query, memory_format=torch.contiguous_format)
+    if video > 0:
+        # rows video..kv-1 are text queries; the bf16 call below overwrites them
+        qz = ops.quantize_qkv(query[:, :, :kv], key[:, :, :kv], value[:, :, :kv])
+        ops.flash_fwd_q8(qz, return_lse=False, out=out[:, :, :kv])
+    if video < S:
+        ops.flash_fwd(query[:, :, video:], key[:, :, :kv], value[:, :, :kv], return_lse=False,
+                      out=out[:, :, video:])
     return out
 
 
@@ -375,7 +395,9 @@ def SparseAttentionWithMap(
     warmup steps.
     """
     if use_dense:
-        output = _dense_engine(query, key, value, pre_defined_mask)
+        output = _dense_engine(query, key, value, pre_defined_mask,
+                               video_token_num=warmup_state.get("video_token_num", 0),
+                               precision=warmup_state.get("precision", "bf16"))
         return output, {"mode": "warmup", "mask": None}
     sparse_type = warmup_state["sparse_type"]
     if sparse_type != "mod-dit":

@@ -5,10 +5,12 @@ Same keys and validation as the reference, plus keys of this build:
                128-row query tile over the union of both rows' key blocks, as the
                reference's engine does (MoD/mod/attn_mask.py:299-303);
                'exact': 64x64 blocks are honoured exactly.
-  'precision'  arithmetic of the sparse steps' attention: 'bf16' (default; bf16 MFMA,
-               fp32 softmax) or 'int8' (int8 Q.K^T with smoothed K, fp8 e4m3 P.V: the
-               SageAttention2-style numerics of the reference's engine,
-               MoD/mod/attn_mask.py:306,312-317). Map steps always run bf16.
+  'precision'  arithmetic of the engine's attention on sparse steps and on
+               use_dense calls: 'bf16' (default; bf16 MFMA, fp32 softmax) or 'int8'
+               (int8 Q.K^T with smoothed K, fp8 e4m3 P.V: the SageAttention2-style
+               numerics of the reference's engine, whose dense branch calls sageattn and
+               sparse branch block_sparse_sage2_attn_cuda, MoD/mod/attn_mask.py:271-276,
+               306,312-317). Map steps always run bf16.
   '_tiles'     the attention tile lists built together with 'mask'.
 """
 from __future__ import annotations

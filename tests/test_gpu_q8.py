@@ -216,6 +216,45 @@ def test_engine_int8_precision(layout):
         md.AttentionSparseEngine(q, k, v, torch.from_numpy(m).to(DEV), precision="fp4")
 
 
+@pytest.mark.parametrize("layout", ["wan", "hunyuan"])
+def test_use_dense_int8_precision(layout):
+    """SparseAttentionWithMap(use_dense=True) under precision='int8': the reference builds an
+    all-True mask and its engine takes the dense branch, sageattn over the valid keys
+    (MoD/mod/attn_mask.py:598-609,268-276), so the video queries run the quantised
+    kernels with K smoothed by the mean of the valid keys only; Hunyuan text queries stay
+    bf16 (its flashinfer call). Under precision='bf16' the call is the bf16 dense kernel."""
+    import mod_dit_amd as md
+    H, D, bs = 2, 128, 64
+    if layout == "wan":
+        video, text, valid = 1920, 0, 1920
+    else:
+        video, text, valid = 1536, 256, 1536 + 150
+    S = video + text
+    q, k, v = (_randn((1, H, S, D), 80 + i, torch.bfloat16) for i in range(3))
+    pdm = None
+    if layout == "hunyuan":
+        pdm = torch.zeros(S, S, dtype=torch.bool, device=DEV)
+        pdm[:, :valid] = True
+    outs = {}
+    for prec in ("int8", "bf16"):
+        st = md.create_adaptive_mask_state(layout, H, video, text, 384, video // 384,
+                                           warmup_steps=4, block_size=bs, precision=prec)
+        outs[prec], info = md.SparseAttentionWithMap(q, k, v, st, None, pre_defined_mask=pdm,
+                                                     current_step=0, use_dense=True)
+        assert info == {"mode": "warmup", "mask": None}
+    qz = ops.quantize_qkv(q[:, :, :valid], k[:, :, :valid], v[:, :, :valid])
+    ref_q, _ = O.attention_q8(_z_np(qz))
+    _check(outs["int8"][0, :, :video], ref_q[:, :video], f"use_dense int8 {layout} video rows",
+           4e-3, 2e-4)
+    ref, _ = O.masked_attention(_np(q[0]), _np(k[0, :, :valid]), _np(v[0, :, :valid]), None,
+                                dtype=np.float64)
+    _check(outs["bf16"][0], ref, f"use_dense bf16 {layout}", 2e-2, 2e-3)
+    if text:
+        assert torch.equal(outs["int8"][0, :, video:], outs["bf16"][0, :, video:])
+    # the quantised rows differ from the bf16 ones: the int8 path really ran
+    assert not torch.equal(outs["int8"][0, :, :video], outs["bf16"][0, :, :video])
+
+
 def test_schedule_int8_precision_cogvideox_shifted_grid():
     """create_adaptive_mask_state(precision='int8'): sparse steps of an unaligned CogVideoX
     layout (grid starting 14 tokens before the text) run the quantised kernels on the

@@ -215,6 +215,19 @@ def test_product_path_refuses_cpu_tensors():
         md.solve_lstsq(st, torch.zeros(1, 4, 4, dtype=torch.float16), 11, 2)
 
 
+def test_use_dense_int8_rejects_more_video_queries_than_valid_keys():
+    """The int8 dense path quantises the first valid-key-count tokens together; more
+    video queries than valid keys is refused before any launch."""
+    S, video = 512, 384
+    st = md.create_adaptive_mask_state("hunyuan", 1, video, S - video, 128, 3, block_size=64,
+                                       precision="int8")
+    pdm = torch.zeros(S, S, dtype=torch.bool)
+    pdm[:, :300] = True  # fewer valid keys than video tokens
+    q = torch.zeros(1, 1, S, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="video_token_num=384"):
+        md.SparseAttentionWithMap(q, q, q, st, None, pre_defined_mask=pdm, use_dense=True)
+
+
 def _fake_amdsmi(samples, cap_uw=1_400_000_000):
     """A stand-in amdsmi module that serves `samples` (power W, clock MHz) in order."""
     it = iter(samples)
