@@ -393,7 +393,9 @@ def _check_q8_call(call, layout, bs, tile_rows, video, valid, tag):
 @pytest.mark.parametrize("layout", ["wan", "hunyuan"])
 def test_processors_with_int8_precision(layout):
     """The same call sites with create_adaptive_mask_state(precision='int8'): sparse steps
-    run the quantised kernels (the reference engine's numerics), every other step bf16."""
+    run the quantised kernels (the reference engine's numerics), and so do the Wan
+    processor's dense steps, which reach the engine's sageattn branch through use_dense;
+    map steps and the Hunyuan processor's SDPA dense steps stay bf16."""
     H, D, tpf, bs = 2, 64, 512, 64
     W, T, top_k, thr = 4, 3, 30, 1e-3
     rec = Recorder()
@@ -435,7 +437,7 @@ def test_processors_with_int8_precision(layout):
                 x = (torch.randn(1, video, C, generator=g) * 0.5 + pos).to(torch.bfloat16).to(DEV)
                 e = torch.randn(1, text, Ce, generator=g).to(torch.bfloat16).to(DEV)
                 proc(attn, x, e, amask, rot)
-    n_sparse = 0
+    n_sparse = n_dense_q8 = 0
     for call in rec.calls:
         st = call["state"]
         phase = "dense" if call["use_dense"] else O.step_phase(call["step"], st["warmup_steps"],
@@ -444,11 +446,20 @@ def test_processors_with_int8_precision(layout):
         if phase == "sparse":
             _check_q8_call(call, layout, bs, st["tile_rows"], video, valid, tag)
             n_sparse += 1
+        elif phase == "dense" and layout == "wan":
+            qz = ops.quantize_qkv(call["q"], call["k"], call["v"])
+            z = {n: getattr(qz, n)[0].cpu().numpy() for n in
+                 ("q8", "q_scale", "k8", "k_scale", "v8t", "v_scale", "k_mean", "q_kmean")}
+            ref_q8, _ = O.attention_q8(z)
+            err = np.abs(_np(call["out"][0]).astype(np.float64) - ref_q8)
+            assert err.max() <= 4e-3 and err.mean() <= 2e-4, (tag, err.max(), err.mean())
+            n_dense_q8 += 1
         else:
             ref, sparse = _expected(call, layout, bs, st["tile_rows"], video, S - video,
                                     valid=None if layout == "wan" else valid)
             _check(call["out"][0], ref, tag, sparse)
     assert n_sparse >= 2
+    assert n_dense_q8 == (4 if layout == "wan" else 0)  # steps 0, 1 of both branches
 
 
 @pytest.mark.parametrize("tile_rows,dtype", [("exact", torch.bfloat16), ("union", torch.bfloat16),
