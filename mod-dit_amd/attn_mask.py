@@ -456,10 +456,13 @@ def SparseAttentionWithMap(
         warmup_state["_tiles_for"] = next_mask
     else:
         mask = warmup_state["mask"]
+        union = warmup_state.get("tile_rows", "union") == "union"
         tiles = warmup_state.get("_tiles") if warmup_state.get("_tiles_for") is mask else None
+        if tiles is not None and tiles.union_rows != union:
+            tiles = None  # built for the other row granularity; the engine rebuilds them
         output = _engine(query, key, value, mask, tiles, pre_defined_mask,
                          warmup_state.get("video_token_num", 0), warmup_state["block_size"],
-                         warmup_state.get("tile_rows", "union") == "union",
+                         union,
                          grid_origin=_grid(warmup_state, seq_len)[3],
                          precision=warmup_state.get("precision", "bf16"))
     return output, {"mask": warmup_state["mask"]}
