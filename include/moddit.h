@@ -194,8 +194,9 @@ int moddit_sparsity_map(const void* q, const void* k, const float* lse, void* ma
  *   [2n-1, 3n-1) column sums
  *   3n-1        sum over the n/bpf frame-diagonal bpf x bpf blocks
  * map: contiguous (H,n,n) of map_dtype.
- *   FP16 (n <= 2^20): one pass over the map, summed exactly in int64 units of 2^-24 and
- *        rounded once to fp32 (deterministic); needs a workspace of
+ *   FP16 (n <= 2^20 and n * min(blocks_per_frame, n) <= 2^23, so that every sum of
+ *        fp16 values stays inside int64): one pass over the map, summed exactly in
+ *        int64 units of 2^-24 and rounded once to fp32 (deterministic); needs a workspace of
  *        moddit_mts_workspace_bytes(heads, n) bytes, 16-byte aligned (scratch);
  *   FP32: summed in fp64 and rounded once; workspace may be NULL.
  * Replaces compute_mts (MoD/mod/cuda_lstsq_kernel.cu:421-482, kernels :17-162).

@@ -349,9 +349,15 @@ def _dense_engine(query, key, value, pre_defined_mask, video_token_num=0, precis
     video = int(video_token_num)
     if not 0 <= video <= kv:
         raise ValueError(f"video_token_num={video} must lie in [0, valid keys={kv}]")
+    if video % 32:
+        # Q is quantised in 32-row blocks: a block straddling the video/text boundary would
+        # take its scale from text rows too, where the reference quantises query[:video]
+        raise ValueError(f"video_token_num={video} must be a multiple of 32 for the int8 path")
     out = torch.empty_like(query, memory_format=torch.contiguous_format)
     if video > 0:
-        # rows video..kv-1 are text queries; the bf16 call below overwrites them
+        # rows video..kv-1 are text queries (every 32-row block lies on one side of the
+        # boundary, so the video rows' scales are those of query[:video] alone); the bf16
+        # call below overwrites them
         qz = ops.quantize_qkv(query[:, :, :kv], key[:, :, :kv], value[:, :, :kv])
         ops.flash_fwd_q8(qz, return_lse=False, out=out[:, :, :kv])
     if video < S:

@@ -146,7 +146,12 @@ constexpr int kMts1TileC = kMts1ColThreads * kMts1Cols;      // 256
 constexpr int kMts1TileR = kMts1Slabs * kMts1Slab;           // 512
 constexpr int kMts1Diag = kMts1Cols + kMts1Sub - 1;          // 23
 constexpr int kMts1TileDiag = kMts1TileC + kMts1TileR - 1;   // 767
-constexpr int kMts1MaxN = 1 << 20;  // int64 units: |sum| <= n * 2^40 stays below 2^63
+// Exactness of the int64 accumulators: an fp16 value is below 2^16, i.e. 2^40 units of
+// 2^-24, so a sum over c cells stays below 2^63 while c <= 2^23. Diagonal and column
+// outputs sum n cells; the frame-block output sums (n / bpf) * bpf^2 = n * min(bpf, n)
+// cells, which the entry point bounds (kMts1MaxFrameCells).
+constexpr int kMts1MaxN = 1 << 20;
+constexpr int64_t kMts1MaxFrameCells = int64_t{1} << 23;
 
 struct Mts1Params {
   const uint16_t* map;
@@ -891,6 +896,12 @@ extern "C" int moddit_mts(const void* map, int map_dtype, int heads, int n, int 
                      "moddit_mts_workspace_bytes(heads, n) bytes");
     MODDIT_CHECK_ARG(aligned16(workspace), "mts: workspace must be 16-byte aligned");
     MODDIT_CHECK_ARG(n <= kMts1MaxN, "mts: n=%d exceeds %d", n, kMts1MaxN);
+    MODDIT_CHECK_ARG(static_cast<int64_t>(n) * (blocks_per_frame < n ? blocks_per_frame : n) <=
+                         kMts1MaxFrameCells,
+                     "mts: n * min(blocks_per_frame, n) = %lld frame-block cells exceed %lld "
+                     "(the exact fp16 sum's int64 range)",
+                     static_cast<long long>(n) * (blocks_per_frame < n ? blocks_per_frame : n),
+                     static_cast<long long>(kMts1MaxFrameCells));
     Mts1Params q;
     q.map = static_cast<const uint16_t*>(map);
     q.heads = heads;

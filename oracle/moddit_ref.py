@@ -19,6 +19,7 @@ __all__ = [
     "masked_attention",
     "probability_map", "replay_map", "replay_map_rows", "refresh_merge", "step_phase", "video_layout",
     "cogvideox_grid", "e4m3_decode", "e4m3_encode", "quantize_qkv", "attention_q8",
+    "attention_q8_with_bound", "q8_exact_error_bound", "e4m3_flip_candidates",
     "MODE_SPARSE", "MODE_BLOCK_DIAGONAL", "MODE_FULL",
 ]
 
@@ -653,6 +654,49 @@ def attention_q8(qz: Dict[str, np.ndarray], token_mask: Optional[np.ndarray] = N
     unrounded P, earlier tiles rescaled by 2^(m_old - m_new); O times v_scale.
     LSE (natural log) = ln(sum P) + (m - shift) ln 2 + scale * q_kmean.
     Returns (O (H, S, D), LSE (H, S)); rows without keys: O = 0, LSE = -inf."""
+    out, lse, _ = _attention_q8_core(qz, token_mask, scale, slack, shift, origin, False, False)
+    return out, lse
+
+
+def e4m3_flip_candidates(p: np.ndarray, tol: np.ndarray) -> np.ndarray:
+    """True where a non-negative value p could round to another e4m3 code than its own
+    under a relative change of at most tol: p (1 - tol) and p (1 + tol) round to
+    different codes (the rounding is monotone, so every value in between rounds to one
+    of those two)."""
+    p = np.asarray(p, np.float64)
+    return e4m3_encode(p * (1 - tol)) != e4m3_encode(p * (1 + tol))
+
+
+def attention_q8_with_bound(qz: Dict[str, np.ndarray], token_mask: Optional[np.ndarray] = None,
+                            scale: Optional[float] = None, slack: float = 1.5,
+                            shift: float = 7.0, origin: int = 0, emulate_fp32: bool = False,
+                            p_jitter: float = 0.0, jitter_seed: int = 0):
+    """`attention_q8` plus, per output element, a bound on how far an implementation of
+    the same arithmetic in fp32 (the kernel) can be from this fp64 model:
+
+      - a weight P whose fp64 value lies within fp32's error of an e4m3 rounding midpoint
+        (P * (1 -/+ tol) round to different codes, tol = 4e-6 (1 + |s|): the score's fp32
+        roundings and exp2's ulp, ~30x over) may round one code the other way: up to
+        2^-3 (1 + 2^-4) P |v8| for a normal P, one subnormal step 2^-9 |v8| below 2^-6;
+      - a row whose lazy-max decision (tile max > m + slack) lies within 4e-6 (1 + |m|)
+        of its threshold may move its max at another tile, after which every P of the row
+        can round the other way: 2^-3 (1 + 2^-4) sum_j P_j |v8_j| for that row;
+      - fp32 accumulation of O and of the row sum l: (keys + 2 tiles + 256) 2^-24
+        relative to |O| + sum_j P_j |v8_j| v_scale / l (recursive-summation bound);
+      - the kernel's bf16 output rounding: 2^-9 of |O| plus the terms above, taken as
+        2^-8 |O| + 2^-8 (terms).
+    All P terms are rescaled with the accumulator and divided by l like O.
+    emulate_fp32: compute the scores and exp2 in fp32 (an fp32 rendering of the same
+    arithmetic, used on the CPU to exercise the bound); p_jitter: multiply every P by
+    1 + p_jitter * U(-1, 1) (seeded) before it is rounded and summed (another rendering
+    whose P differ by up to p_jitter, for the same purpose; the bound itself is computed
+    from the unperturbed model). Returns (O, LSE, bound)."""
+    return _attention_q8_core(qz, token_mask, scale, slack, shift, origin, True, emulate_fp32,
+                              p_jitter, jitter_seed)
+
+
+def _attention_q8_core(qz, token_mask, scale, slack, shift, origin, want_bound, fp32,
+                       p_jitter=0.0, jitter_seed=0):
     q8 = qz["q8"].astype(np.float64)
     k8 = qz["k8"].astype(np.float64)
     H, S, D = q8.shape
@@ -665,35 +709,153 @@ def attention_q8(qz: Dict[str, np.ndarray], token_mask: Optional[np.ndarray] = N
     vs = qz["v_scale"].astype(np.float64)
     out = np.zeros((H, S, D))
     lse = np.full((H, S), -np.inf)
+    bound = np.zeros((H, S, D)) if want_bound else None
     nt = (S - origin + 63) // 64
+    f32 = np.float32
+    jrng = np.random.default_rng(jitter_seed)
     for h in range(H):
-        s_all = (q8[h] @ k8[h].T) * qs[h][:, None] * ks[h][None, :] * scale * np.log2(np.e)
+        if fp32:
+            s_all = (((q8[h] @ k8[h].T).astype(f32) * qs[h][:, None].astype(f32))
+                     * ks[h][None, :].astype(f32)) * f32(scale * np.log2(np.e))
+            s_all = s_all.astype(np.float64)
+        else:
+            s_all = (q8[h] @ k8[h].T) * qs[h][:, None] * ks[h][None, :] * scale * np.log2(np.e)
         if token_mask is not None:
             s_all = np.where(token_mask[h], s_all, -np.inf)
         m = np.full(S, -np.inf)
         acc = np.zeros((S, D))
         l = np.zeros(S)
+        av = np.abs(v[h])
+        if want_bound:
+            flip_acc = np.zeros((S, D))
+            tot_acc = np.zeros((S, D))
+            near_max = np.zeros(S, bool)
+            n_keys = np.zeros(S)
+            n_tiles = np.zeros(S)
         for t in range(nt):
             k0, k1 = max(origin + 64 * t, 0), min(origin + 64 * t + 64, S)
             st = s_all[:, k0:k1]
             mx = st.max(axis=1)
             act = np.isfinite(mx)  # rows for which this tile holds a key
             need = act & (mx > m + slack)
+            if want_bound:
+                fin_m = np.isfinite(m)
+                gap = np.where(act & fin_m, mx - np.where(fin_m, m, 0) - slack, np.inf)
+                near_max |= np.abs(gap) <= 4e-6 * (1 + np.abs(np.where(act, mx, 0)))
             m_new = np.where(need, mx, m)
             fin_new = np.where(np.isfinite(m_new), m_new, 0)
             alpha = np.where(np.isfinite(m), np.exp2(np.where(np.isfinite(m), m - fin_new, 0)), 0.0)
             alpha = np.where(act, np.where(need, alpha, 1.0), 1.0)
-            p = np.where(act[:, None], np.exp2(st - (fin_new - shift)[:, None]), 0.0)
+            arg = st - (fin_new - shift)[:, None]
+            if fp32:
+                p = np.where(act[:, None], np.exp2(arg.astype(f32)).astype(np.float64), 0.0)
+            else:
+                p = np.where(act[:, None], np.exp2(arg), 0.0)
+            p_model = p
+            if p_jitter:
+                p = p * (1 + p_jitter * jrng.uniform(-1, 1, p.shape))
             p8 = e4m3_decode(e4m3_encode(p))
             acc = acc * alpha[:, None] + p8 @ v[h, k0:k1]
             l = l * alpha + p.sum(axis=1)
+            if want_bound:
+                p = p_model
+                keyed = np.isfinite(st)
+                tol = 4e-6 * (1 + np.abs(np.where(keyed, st, 0)))
+                flip = e4m3_flip_candidates(p, tol) & keyed
+                step = np.maximum(2.0 ** -3 * (1 + 2.0 ** -4) * p, 2.0 ** -9)
+                flip_acc = flip_acc * alpha[:, None] + np.where(flip, step, 0.0) @ av[k0:k1]
+                tot_acc = tot_acc * alpha[:, None] + p @ av[k0:k1]
+                n_keys += keyed.sum(axis=1)
+                n_tiles += act
             m = m_new
         o = acc * vs[h][None, :]
         ok = l > 0
-        out[h] = np.where(ok[:, None], o / np.where(ok, l, 1)[:, None], 0)
+        linv = np.where(ok, 1.0 / np.where(ok, l, 1), 0.0)[:, None]
+        out[h] = o * linv
         lse[h] = np.where(ok, np.log(np.where(ok, l, 1)) + (np.where(ok, m, 0) - shift) * np.log(2)
                           + scale * qz["q_kmean"][h], -np.inf)
-    return out, lse
+        if want_bound:
+            tot = tot_acc * vs[h][None, :] * linv
+            flip_o = np.where(near_max[:, None], 2.0 ** -3 * (1 + 2.0 ** -4) * tot,
+                              flip_acc * vs[h][None, :] * linv)
+            gam = (n_keys + 2 * n_tiles + 256)[:, None] * 2.0 ** -24
+            terms = flip_o + gam * (np.abs(out[h]) + tot)
+            bound[h] = terms * (1 + 2.0 ** -8) + 2.0 ** -8 * np.abs(out[h])
+    return out, lse, bound
+
+
+def q8_exact_error_bound(q, k, v, q8, q_scale, k8, k_scale, k_mean, v_scale,
+                         allowed: Optional[np.ndarray] = None, scale: Optional[float] = None,
+                         drop: Sequence[str] = ()):
+    """Exact attention of query rows q (R, D) over keys k, v (S, D) (the unquantised bf16
+    values, fp64), and a bound on how far the int8 Q.K^T / fp8 P.V kernel's output can be
+    from it, per element, derived from the rounding model of that arithmetic:
+
+    q8 (R, D) int8 with per-row q_scale (R,) (each row's 32-row block scale), k8 (S, D)
+    int8 with per-key k_scale (S,) (its 64-key tile's scale), k_mean (D,), v_scale (D,):
+    the quantiser's outputs for these rows and keys. allowed (R, S): the executed mask.
+
+      - int8 scores: the kernel's scores s8 = scale q8.k8 q_scale k_scale against the
+        exact smoothed scores s = scale q.(k - k_mean) (the constant q.k_mean shift cancels
+        in softmax) differ by e_j; with E = (max_j e_j - min_j e_j) / 2 over the row's keys
+        plus 1e-5 (1 + max|s8|) for the kernel's fp32 scores and exp2, the weights satisfy
+        w8_j / w_j in [e^-2E, e^2E], so sum_j (w8_j - w_j) v_j <= (e^2E - 1) sum_j w_j |v_j|;
+      - e4m3 P and e4m3 V: each 2^-4 relative (normal values), so the P.V sum over the
+        fp32 row sum of the unrounded P is off by <= (2^-3 + 2^-8) sum_j w8_j |v_j|, with
+        sum_j w8_j |v_j| <= e^2E sum_j w_j |v_j|; below e4m3's normal range an absolute
+        error instead: V below 2^-6 v_scale: 2^-10 v_scale (twice, both factors); P below
+        2^-6: 2^-10 (1 + 2^-4) |v_j| / l with l >= 2^7 (P = 2^(y - m + 7), the lazy max
+        m <= the row max y_max), for keys with y_j < y_max - 13 (log2 units) only;
+      - fp32 accumulation (O and l over the keys): (keys + 2 tiles + 256) 2^-24 relative
+        to |o| + 2 e^2E sum_j w_j |v_j|;
+      - bf16 output rounding: 2^-9 of |o| plus all the above.
+    drop: names of terms to leave out ("score", "e4m3", "subnormal", "accumulation",
+    "output"), for tests that show each one is needed.
+    Returns (o (R, D), bound (R, D), E (R,))."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    R, D = q.shape
+    S = k.shape[0]
+    if scale is None:
+        scale = D ** -0.5
+    if allowed is None:
+        allowed = np.ones((R, S), bool)
+    s = scale * (q @ (k - np.asarray(k_mean, np.float64)[None, :]).T)
+    s8 = scale * (np.asarray(q8, np.float64) @ np.asarray(k8, np.float64).T) \
+        * np.asarray(q_scale, np.float64)[:, None] * np.asarray(k_scale, np.float64)[None, :]
+    e = np.where(allowed, s8 - s, np.nan)
+    has = allowed.any(axis=1)
+    E = np.where(has, (np.nanmax(np.where(has[:, None], e, 0), axis=1)
+                       - np.nanmin(np.where(has[:, None], e, 0), axis=1)) / 2, 0.0)
+    s8a = np.where(allowed, s8, -np.inf)
+    E = E + 1e-5 * (1 + np.abs(np.where(allowed, s8, 0)).max(axis=1))
+    sa = np.where(allowed, s, -np.inf)
+    mx = np.where(has, sa.max(axis=1), 0)
+    w = np.where(allowed, np.exp(sa - mx[:, None]), 0.0)
+    w = w / np.where(has, w.sum(axis=1), 1)[:, None]
+    av = np.abs(v)
+    o = w @ v
+    bv = w @ av
+    y = s8a * np.log2(np.e)
+    ymax = np.where(has, y.max(axis=1), 0)
+    sub = allowed & (y < (ymax - 12.99)[:, None])
+    sub_v = sub.astype(np.float64) @ av
+    n_sub = sub.sum(axis=1)[:, None]
+    keys = allowed.sum(axis=1)
+    gam = ((keys + 2 * ((keys + 63) // 64) + 256) * 2.0 ** -24)[:, None]
+    vsc = np.asarray(v_scale, np.float64)[None, :]
+    grow = np.exp(2 * E)[:, None]
+    on = {t: 0.0 if t in drop else 1.0
+          for t in ("score", "e4m3", "subnormal", "accumulation", "output")}
+    pre = (on["score"] * (grow - 1) * bv
+           + on["e4m3"] * grow * (2.0 ** -3 + 2.0 ** -8) * bv
+           + on["subnormal"] * (grow * 2.0 ** -9 * vsc
+                                + 2.0 ** -17 * (1 + 2.0 ** -4) * (sub_v + n_sub * vsc * 2.0 ** -10))
+           + on["accumulation"] * gam * (np.abs(o) + 2 * grow * bv))
+    out_r = on["output"] * 2.0 ** -9
+    bound = np.where(has[:, None], pre * (1 + out_r) + out_r * np.abs(o), 0.0)
+    return o, bound, E
 
 
 def refresh_merge(prev: np.ndarray, cur: np.ndarray, mask: np.ndarray) -> np.ndarray:

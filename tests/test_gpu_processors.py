@@ -33,6 +33,7 @@ import torch
 import mod_dit_amd as md
 import oracle as O
 from mod_dit_amd import ops
+from q8_contract import check_q8_model
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -378,11 +379,8 @@ def _check_q8_call(call, layout, bs, tile_rows, video, valid, tag):
     else:
         _, lists = O.tiles_from_mask(mask, bs, union)
         tm[:] = O.token_mask_from_tiles(lists, H, S, S)
-    ref_q8, _ = O.attention_q8(z, tm)
-    got = _np(call["out"][0]).astype(np.float64)
-    err = np.abs(got[:, :video] - ref_q8[:, :video])
-    print(f"{tag} int8 video rows: max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
-    assert err.max() <= 4e-3 and err.mean() <= 2e-4, (tag, err.max(), err.mean())
+    check_q8_model(call["out"][0][:, :video], z, tm, rows=slice(0, video),
+                   tag=f"{tag} int8 video rows")
     if video < S:
         tt = np.zeros((H, S, S), bool)
         tt[:, :, :valid] = True
@@ -450,9 +448,7 @@ def test_processors_with_int8_precision(layout):
             qz = ops.quantize_qkv(call["q"], call["k"], call["v"])
             z = {n: getattr(qz, n)[0].cpu().numpy() for n in
                  ("q8", "q_scale", "k8", "k_scale", "v8t", "v_scale", "k_mean", "q_kmean")}
-            ref_q8, _ = O.attention_q8(z)
-            err = np.abs(_np(call["out"][0]).astype(np.float64) - ref_q8)
-            assert err.max() <= 4e-3 and err.mean() <= 2e-4, (tag, err.max(), err.mean())
+            check_q8_model(call["out"][0], z, tag=f"{tag} int8 dense")
             n_dense_q8 += 1
         else:
             ref, sparse = _expected(call, layout, bs, st["tile_rows"], video, S - video,

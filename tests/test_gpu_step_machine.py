@@ -15,6 +15,7 @@ import torch
 import mod_dit_amd as md
 import oracle as O
 from mod_dit_amd import ops
+from q8_contract import check_q8_model
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -325,8 +326,7 @@ def test_cogvideox_128_blocks_grid_starting_beyond_64_tokens(precision):
                       k8=qz.k8[0].cpu().numpy(), k_scale=qz.k_scale[0].cpu().numpy(),
                       v8t=qz.v8t[0].cpu().numpy(), v_scale=qz.v_scale[0].cpu().numpy(),
                       k_mean=qz.k_mean[0].cpu().numpy(), q_kmean=qz.q_kmean[0].cpu().numpy())
-            ref, _ = O.attention_q8(zn, tm, origin=origin + 64)
-            err = np.abs(_np(out[0]).astype(np.float64) - ref)
-            assert err.max() <= 4e-3 and err.mean() <= 3e-4, (step, err.max(), err.mean())
+            check_q8_model(out[0], zn, tm, origin=origin + 64,
+                           tag=f"cogvideox bs=128 origin={origin} int8 step {step}")
         checked += 1
     assert checked == 2

@@ -132,6 +132,11 @@ def test_c_abi_rejects_bad_arguments_before_any_launch():
     assert rc == _lib.MODDIT_EINVAL and b"exceeds" in lib.moddit_last_error()
     rc = lib.moddit_mts(P, _lib.FP16, 1, 64, 4, P + 8, P, None)
     assert rc == _lib.MODDIT_EINVAL and b"aligned" in lib.moddit_last_error()
+    # the frame-block output sums n * min(bpf, n) cells: at most 2^23 stay exact in int64
+    rc = lib.moddit_mts(P, _lib.FP16, 1, 4096, 4096, P, P, None)
+    assert rc == _lib.MODDIT_EINVAL and b"frame-block cells" in lib.moddit_last_error()
+    rc = lib.moddit_mts(P, _lib.FP16, 1, 4096, 2049, P, P, None)
+    assert rc == _lib.MODDIT_EINVAL and b"frame-block cells" in lib.moddit_last_error()
     with pytest.raises(_lib.ModditError, match="mtm"):
         _lib.check(lib.moddit_mtm_host(-1, 1, 1.0, None), "moddit_mtm_host")
 
@@ -225,6 +230,20 @@ def test_use_dense_int8_rejects_more_video_queries_than_valid_keys():
     pdm[:, :300] = True  # fewer valid keys than video tokens
     q = torch.zeros(1, 1, S, 64, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="video_token_num=384"):
+        md.SparseAttentionWithMap(q, q, q, st, None, pre_defined_mask=pdm, use_dense=True)
+
+
+def test_use_dense_int8_rejects_a_q_block_across_the_video_text_boundary():
+    """Q is quantised in 32-row blocks; with a video length that is not a multiple of 32
+    one block would mix video and text rows (the reference quantises query[:video]
+    alone), so the int8 dense path refuses it before any launch."""
+    S, video = 512, 400
+    st = md.create_adaptive_mask_state("hunyuan", 1, video, S - video, 80, 5, block_size=16,
+                                       precision="int8")
+    pdm = torch.zeros(S, S, dtype=torch.bool)
+    pdm[:, :450] = True
+    q = torch.zeros(1, 1, S, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="multiple of 32"):
         md.SparseAttentionWithMap(q, q, q, st, None, pre_defined_mask=pdm, use_dense=True)
 
 

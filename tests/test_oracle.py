@@ -524,3 +524,134 @@ def test_video_mask_cells_equal_the_line_by_line_restatement(n, bpf, k):
     for h in (0, 1):  # and the scalar cell definition on a sample of cells
         for i, j in rng.integers(0, n, size=(50, 2)):
             assert want[h, i, j] == O.mask_cell(sel[h], modes[h], n, bpf, i, j)
+
+
+# --------------------------------------------------------------------------------------
+# error bounds of the int8/fp8 path (the GPU tests' contracts)
+# --------------------------------------------------------------------------------------
+def test_e4m3_flip_candidates_flag_every_value_a_small_change_can_reround():
+    codes = O.e4m3_decode(np.arange(1, 126))  # positive finite codes
+    mids = (codes[:-1] + codes[1:]) / 2
+    tol = np.full(mids.shape, 1e-6)
+    assert O.e4m3_flip_candidates(mids, tol).all()  # rounding midpoints
+    assert not O.e4m3_flip_candidates(codes[1:-1], np.full(codes.size - 2, 1e-6)).any()
+    assert not O.e4m3_flip_candidates(mids * (1 + 3e-6), tol).any()  # beyond tol
+    # the property the kernel bound rests on: any relative change up to tol that changes
+    # the rounding happens only at a flagged value
+    rng = np.random.default_rng(21)
+    p = np.exp2(rng.uniform(-12, 8.5, 200000))
+    p[:5000] = mids[rng.integers(0, mids.size, 5000)] * (1 + rng.uniform(-5e-6, 5e-6, 5000))
+    tol = 4e-6
+    delta = rng.uniform(-tol, tol, p.size)
+    moved = O.e4m3_encode(p * (1 + delta)) != O.e4m3_encode(p)
+    assert moved.sum() > 100
+    assert np.all(O.e4m3_flip_candidates(p, np.full(p.size, tol))[moved])
+
+
+def _q8_case(seed, S=512, D=64, qscale=1.0, keys_per_row=None, density=1.0, origin=0):
+    rng = np.random.default_rng(seed)
+    q = O.bf16_round(rng.standard_normal((1, S, D)) * qscale)
+    k = O.bf16_round(rng.standard_normal((1, S, D)) + 0.5)
+    v = O.bf16_round(rng.standard_normal((1, S, D)))
+    if keys_per_row is None:
+        tm = rng.random((1, S, S)) < density
+    else:
+        tm = np.zeros((1, S, S), bool)
+        for r in range(S):
+            tm[0, r, rng.choice(S, keys_per_row, replace=False)] = True
+    tm[:, :, 0] |= ~tm.any(axis=2)
+    return q, k, v, tm, origin
+
+
+_Q8_CASES = [dict(seed=1), dict(seed=2, keys_per_row=3, qscale=2.0),
+             dict(seed=3, D=128, qscale=2.0, density=0.3),
+             dict(seed=4, qscale=4.0, density=0.1, origin=-14)]
+
+
+@pytest.mark.parametrize("case", range(len(_Q8_CASES)))
+def test_q8_model_bound_covers_fp32_renderings_and_catches_larger_errors(case):
+    # The kernel-vs-model contract: renderings of the same arithmetic whose P differ from
+    # the fp64 model's by less than the flip tolerance (fp32 scores and exp2; a seeded
+    # relative jitter of 2e-6) stay inside attention_q8_with_bound's bound; P errors of
+    # 1e-3 (250x the tolerance) re-round weights that the bound does not allow for.
+    q, k, v, tm, origin = _q8_case(**_Q8_CASES[case])
+    z = O.quantize_qkv(q, k, v, origin=origin)
+    o, lse, b = O.attention_q8_with_bound(z, tm, origin=origin)
+    o0, lse0 = O.attention_q8(z, tm, origin=origin)
+    assert np.array_equal(o, o0) and np.array_equal(lse, lse0)
+    o32, _, _ = O.attention_q8_with_bound(z, tm, origin=origin, emulate_fp32=True)
+    assert np.all(np.abs(o32 - o) <= b)
+    oj, _, _ = O.attention_q8_with_bound(z, tm, origin=origin, p_jitter=2e-6, jitter_seed=case)
+    assert np.all(np.abs(oj - o) <= b)
+    ob, _, _ = O.attention_q8_with_bound(z, tm, origin=origin, p_jitter=1e-3, jitter_seed=case)
+    assert (np.abs(ob - o) > b).sum() > 0
+
+
+def _exact_bound(q, k, v, z, tm, origin=0, drop=()):
+    S = q.shape[1]
+    pos = np.arange(S) - origin
+    return O.q8_exact_error_bound(q[0], k[0], v[0], z["q8"][0], z["q_scale"][0][pos // 32],
+                                  z["k8"][0], z["k_scale"][0][pos // 64], z["k_mean"][0],
+                                  z["v_scale"][0], allowed=tm[0], drop=drop)
+
+
+@pytest.mark.parametrize("case", range(len(_Q8_CASES)))
+def test_q8_exact_bound_holds_for_the_modelled_arithmetic(case):
+    # The kernel-vs-exact contract: the model of the kernel's arithmetic (int8 scores,
+    # lazy max, e4m3 P and V, output rounded to bf16 like the kernel's) against exact
+    # attention on the unquantised inputs stays inside q8_exact_error_bound, and not by
+    # orders of magnitude (rows over many keys reach ~0.1 of it: the bound takes the
+    # score errors as coherent; rows over few keys ~0.7).
+    q, k, v, tm, origin = _q8_case(**_Q8_CASES[case])
+    z = O.quantize_qkv(q, k, v, origin=origin)
+    o8, _ = O.attention_q8(z, tm, origin=origin)
+    o8 = O.bf16_round(o8[0].astype(np.float32)).astype(np.float64)
+    o, b, E = _exact_bound(q, k, v, z, tm, origin)
+    ref, _ = O.masked_attention(q, k, v, tm, dtype=np.float64)
+    np.testing.assert_allclose(o, ref[0], rtol=0, atol=1e-12)
+    r = np.abs(o8 - o) / b
+    assert r.max() <= 1.0 and r.max() > 0.05, r.max()
+    assert np.all(E >= 0)
+
+
+def test_q8_exact_bound_needs_each_rounding_term():
+    # Planted omissions: each term of the bound is needed by some input.
+    # (1) e4m3 rounding of P and V: rows with three keys.
+    q, k, v, tm, _ = _q8_case(seed=2, keys_per_row=3, qscale=2.0)
+    z = O.quantize_qkv(q, k, v)
+    o8 = O.bf16_round(O.attention_q8(z, tm)[0][0].astype(np.float32)).astype(np.float64)
+    o, b, _ = _exact_bound(q, k, v, z, tm)
+    _, b_no, _ = _exact_bound(q, k, v, z, tm, drop=("e4m3",))
+    assert np.all(np.abs(o8 - o) <= b) and (np.abs(o8 - o) > b_no).sum() > 100
+    # (2) values below e4m3's normal range: V entries of 1e-5 where the channel max is ~4
+    # (a subnormal step, 2^-9 v_scale, is comparable to the value), read by one key each
+    rng = np.random.default_rng(6)
+    S, D = 256, 64
+    q = O.bf16_round(rng.standard_normal((1, S, D)))
+    k = O.bf16_round(rng.standard_normal((1, S, D)))
+    v = O.bf16_round(rng.standard_normal((1, S, D)))
+    v[:, 10:20] = O.bf16_round(np.full((1, 10, D), 1e-5, np.float32))
+    tm = np.zeros((1, S, S), bool)
+    tm[0, np.arange(S), 10 + np.arange(S) % 10] = True
+    z = O.quantize_qkv(q, k, v)
+    o8 = O.bf16_round(O.attention_q8(z, tm)[0][0].astype(np.float32)).astype(np.float64)
+    o, b, _ = _exact_bound(q, k, v, z, tm)
+    _, b_no, _ = _exact_bound(q, k, v, z, tm, drop=("subnormal",))
+    assert np.all(np.abs(o8 - o) <= b) and (np.abs(o8 - o) > b_no).sum() > 100
+    # (3) int8 scores: a 32-row block with one huge channel (that K leaves at zero) gets
+    # coarse Q steps; rows of two keys with values +-1 turn the score error into output
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((1, S, D)) * 2
+    q[:, ::32, 0] = 100.0
+    k = rng.standard_normal((1, S, D))
+    k[:, :, 0] = 0.0
+    v = rng.standard_normal((1, S, D))
+    q, k, v = (O.bf16_round(x.astype(np.float32)) for x in (q, k, v))
+    tm = np.zeros((1, S, S), bool)
+    for r in range(S):
+        tm[0, r, rng.choice(S, 2, replace=False)] = True
+    z = O.quantize_qkv(q, k, v)
+    o8 = O.bf16_round(O.attention_q8(z, tm)[0][0].astype(np.float32)).astype(np.float64)
+    o, b, _ = _exact_bound(q, k, v, z, tm)
+    _, b_no, _ = _exact_bound(q, k, v, z, tm, drop=("score",))
+    assert np.all(np.abs(o8 - o) <= b) and (np.abs(o8 - o) > b_no).sum() > 100
