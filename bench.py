@@ -16,8 +16,13 @@ The int8/fp8 path (quantiser + int8 Q.K^T / fp8 P.V kernels) is timed on the sam
 and tiles and reported under "q8" (a reported alternative; the headline stays bf16).
 Under "vendor": torch's own scaled_dot_product_attention (flash backend) on the same
 layer's dense attention, and a hipBLASLt bf16 GEMM with its board power and clock.
+Under "other_configs", after the headline's timed region: the headline mask executed
+with union tile rows (the reference engine's 128-row granularity), the 50-step
+denoising trajectory on the headline layer and the Wan-like layer
+(configs[2]), each in compact form.
 
     python bench.py [--steps K] [--warmup W] [--tile-rows union|exact] [--no-cpu] [--no-q8]
+                    [--no-extra]
 """
 from __future__ import annotations
 
@@ -448,8 +453,10 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
     mean_sparse = sum(r["ms"] for r in sparse_rows) / len(sparse_rows)
     mean_over = sum(r["overhead_ms"] for r in sparse_rows) / len(sparse_rows)
     traj_ms = sum(r["ms"] for r in rows)
-    # the all-dense bf16 trajectory is the baseline of every sweep (with int8 dense steps
-    # the steps' own dense time is the int8/fp8 kernel's)
+    # two all-dense baselines: the bf16 dense kernel (the build's own dense attention), and
+    # the all-dense trajectory in the sweep's own dense arithmetic (the int8/fp8 kernel when
+    # the dense steps are quantised, as the reference's sageattn dense branch is); the
+    # speedup over the second is the sparsity's alone
     bf16_dense_ms = dense_ms
     if q8_dense:
         bf16_dense_ms = sorted(time_events(
@@ -459,6 +466,8 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
         "config": {"workload": f"{config}-like layer, 50 steps, W={W}, T={T}, sparsity 50%->90%",
                    "H": H, "N": N, "d": D, "block": bs, "tile_rows": "union" if union else "exact"},
         "dense_ms": round(dense_ms, 3),
+        "dense_ms_is": ("the int8/fp8 dense kernel (the sweep's dense steps)" if q8_dense else
+                        "the bf16 dense kernel"),
         "mean_sparse_step_ms": round(mean_sparse, 3),
         "mean_sparse_overhead_ms": round(mean_over, 4),
         "mean_overhead_frac_of_dense": round(mean_over / dense_ms, 5),
@@ -467,6 +476,9 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
         "trajectory_wall_ms": round(total_ms, 2),
         "all_dense_trajectory_ms": round(bf16_dense_ms * steps, 2),
         "trajectory_speedup_vs_dense": round(bf16_dense_ms * steps / traj_ms, 3),
+        "trajectory_speedup_vs_dense_is": "over the all-dense trajectory on the bf16 dense kernel",
+        "all_dense_same_arithmetic_trajectory_ms": round(dense_ms * steps, 2),
+        "trajectory_speedup_vs_same_arithmetic_dense": round(dense_ms * steps / traj_ms, 3),
         "steps": rows,
         "dtype": ("bf16" if precision == "bf16" else
                   "int8 Q.K^T + fp8 P.V on sparse " + ("and dense steps" if q8_dense else "steps")
@@ -687,6 +699,88 @@ def run_mask_config(name, *, steps, warmup, no_cpu):
 INT8_FP8_PEAK_TFLOPS = 5000.0  # MI355X dense int8 / fp8 MFMA peak
 
 
+# ------------------------------------------------------------------------------------
+# compact legs of the default run: the other configurations under the same clock
+# ------------------------------------------------------------------------------------
+def union_leg(q, k, v, art, *, reps, eff_flop, exact_ms):
+    """The headline layer's mask executed at the reference engine's own granularity:
+    each pair of 64-row mask rows as one 128-row query tile over the union of their key
+    tiles (MoD/mod/attn_mask.py:297-303)."""
+    tiles_u = ops.mask_to_tiles(art["mask"], 64, union_rows=True)
+    pairs = int(tiles_u.active_tile_pairs().sum().item())
+    pairs_exact = int(art["tiles"].active_tile_pairs().sum().item())
+    out = torch.empty_like(q)
+    for _ in range(3):
+        ops.block_sparse_fwd(q, k, v, tiles_u, out=out)
+    ev = time_events(lambda: ops.block_sparse_fwd(q, k, v, tiles_u, out=out), reps)
+    ms = sum(ev) / len(ev)
+    exec_flop = 4.0 * q.shape[3] * 64 * 64 * pairs
+    return {"workload": "headline layer, same mask, tile_rows=union",
+            "ms": round(ms, 4),
+            "effective_tflops": round(eff_flop / (ms * 1e-3) / 1e12, 3),
+            "executed_tflops": round(exec_flop / (ms * 1e-3) / 1e12, 3),
+            "frac": round(exec_flop / (ms * 1e-3) / 1e12 / MI355X_BF16_DENSE_TFLOPS, 4),
+            "executed_pairs": pairs, "executed_pairs_exact_rows": pairs_exact,
+            "ms_over_exact_rows": round(ms / exact_ms, 4)}
+
+
+def trajectory_leg(q, k, v, art, *, H, N, D, bpf, threshold):
+    """The 50-step denoising trajectory on the headline layer,
+    compact: run_sweep's totals without the per-step rows."""
+    r = run_sweep(q, k, v, art, H=H, N=N, D=D, bpf=bpf, bs=64, union=False,
+                  threshold=threshold, config="hunyuan")
+    sparse = [x for x in r["steps"] if x["phase"] == "sparse"]
+    keep = ("trajectory_ms", "all_dense_trajectory_ms", "trajectory_speedup_vs_dense",
+            "dense_ms", "mean_sparse_step_ms", "mean_sparse_overhead_ms",
+            "mean_overhead_frac_of_dense")
+    out = {"workload": r["config"]["workload"]}
+    out.update({key: r[key] for key in keep})
+    out["sparsity_first_last_sparse_step"] = [sparse[0]["sparsity"], sparse[-1]["sparsity"]]
+    out["top_k_first_last_sparse_step"] = [sparse[0]["top_k"], sparse[-1]["top_k"]]
+    return out
+
+
+def layer_leg(name, *, reps, threshold):
+    """Compact figures of another structured layer (CONFIGS[name], here the Wan-like one)
+    with its own predicted mask: block-sparse and dense attention and the per-step mask
+    overhead."""
+    cfg = CONFIGS[name]
+    H, F, Hp, Wp, D = cfg["H"], cfg["F"], cfg["Hp"], cfg["Wp"], cfg["D"]
+    N = F * Hp * Wp
+    bpf = (Hp * Wp) // 64
+    q, k, v = synth_qkv(H, F, Hp, Wp, D, seed=0)
+    art = predict_tiles(q, k, v, block_size=64, bpf=bpf, threshold=threshold,
+                        target_sparsity=cfg["sparsity"], union=False)
+    tiles = art["tiles"]
+    pairs = int(tiles.active_tile_pairs().sum().item())
+    out = torch.empty_like(q)
+    for _ in range(3):
+        ops.block_sparse_fwd(q, k, v, tiles, out=out)
+    ev = time_events(lambda: ops.block_sparse_fwd(q, k, v, tiles, out=out), reps)
+    ms = sum(ev) / len(ev)
+    dn = time_events(lambda: ops.flash_fwd(q, k, v, return_lse=False, out=out), 3)
+    dense_ms = sorted(dn)[1]
+    for _ in range(2):
+        mask_overhead_once(art, bpf=bpf, block_size=64, union=False)
+    ov = time_events(lambda: mask_overhead_once(art, bpf=bpf, block_size=64, union=False), 10)
+    overhead_ms = sorted(ov)[len(ov) // 2]
+    eff_flop = 4.0 * H * N * N * D
+    exec_flop = 4.0 * D * 64 * 64 * pairs
+    res = {"workload": f"{name}-like layer: B=1 H={H} N={N} ({F}x{Hp}x{Wp}) d={D}, 64x64 "
+                       f"blocks, tile_rows=exact",
+           "top_k": art["top_k"], "mask_sparsity": round(art["sparsity"], 5),
+           "sparse_ms": round(ms, 4), "dense_ms": round(dense_ms, 3),
+           "effective_tflops": round(eff_flop / (ms * 1e-3) / 1e12, 3),
+           "executed_tflops": round(exec_flop / (ms * 1e-3) / 1e12, 3),
+           "frac": round(exec_flop / (ms * 1e-3) / 1e12 / MI355X_BF16_DENSE_TFLOPS, 4),
+           "dense_frac": round(eff_flop / (dense_ms * 1e-3) / 1e12 / MI355X_BF16_DENSE_TFLOPS, 4),
+           "speedup_vs_dense": round(dense_ms / ms, 3),
+           "mask_overhead_ms": round(overhead_ms, 4)}
+    del q, k, v, out, art, tiles
+    torch.cuda.empty_cache()
+    return res
+
+
 def q8_leg(q, k, v, tiles, out, *, ref, eff_flop, exec_flop, reps):
     """Timings of the int8/fp8 path on the same layer and tiles: quantiser, block-sparse and
     dense kernels (HIP events on the launch stream), the block-sparse kernel's executed
@@ -736,6 +830,9 @@ def main(argv=None):
     ap.add_argument("--dense-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-q8", action="store_true", help="skip the int8/fp8 path's timings")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the compact legs of the default run (union rows, the 50-step "
+                         "trajectory, the Wan-like layer)")
     ap.add_argument("--precision", choices=("bf16", "int8"), default="bf16",
                     help="--sweep only: arithmetic of the sparse steps (the headline line is bf16)")
     ap.add_argument("--sweep", action="store_true",
@@ -955,6 +1052,18 @@ def main(argv=None):
         q8 = q8_leg(q, k, v, tiles, out, ref=out.clone(), eff_flop=eff_flop, exec_flop=exec_flop,
                     reps=args.steps)
 
+    extra = None
+    if not args.no_extra and args.config == "hunyuan":
+        extra = {}
+        log("headline mask with union tile rows")
+        extra["union_rows"] = union_leg(q, k, v, art, reps=args.steps, eff_flop=eff_flop,
+                                        exact_ms=kernel_ms)
+        log("50-step trajectory on the headline layer")
+        extra["trajectory"] = trajectory_leg(q, k, v, art, H=H, N=N, D=D, bpf=bpf,
+                                             threshold=args.threshold)
+        log("Wan-like layer")
+        extra["wan"] = layer_leg("wan", reps=args.steps, threshold=args.threshold)
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -1051,6 +1160,7 @@ def main(argv=None):
         "vendor": vendor,
         "cpu_baseline": cpu,
         "q8": q8,
+        "other_configs": extra,
         "host": {"cpu_count": os.cpu_count(), "machine": platform.processor() or platform.machine(),
                  "torch": torch.__version__},
     }

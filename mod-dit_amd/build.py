@@ -22,8 +22,9 @@ CSRC = PKG_DIR / "csrc"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_NAME = "libmoddit.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-# measurement aid for bench.py (MFMA ceiling on random operands); not part of the C ABI
-CALIB_SRC = CSRC / "calib" / "mfma_ceiling.hip"
+# measurement aids (MFMA ceiling on random operands for bench.py, single-MFMA accumulation
+# precision for the int8/fp8 accuracy contract); not part of the C ABI
+CALIB_SRCS = (CSRC / "calib" / "mfma_ceiling.hip", CSRC / "calib" / "mfma_precision.hip")
 CALIB_PATH = PKG_DIR / "libmoddit_calib.so"
 
 ARCH = "gfx950"
@@ -84,9 +85,9 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
 
 
 def build_calib(verbose: bool = False) -> Path:
-    """Compile the MFMA-ceiling measurement kernel into libmoddit_calib.so."""
+    """Compile the MFMA measurement kernels into libmoddit_calib.so."""
     tmp = CALIB_PATH.with_suffix(".so.tmp")
-    _run([hipcc(), *COMMON_FLAGS, "-shared", "-o", str(tmp), str(CALIB_SRC)], verbose)
+    _run([hipcc(), *COMMON_FLAGS, "-shared", "-o", str(tmp), *map(str, CALIB_SRCS)], verbose)
     os.replace(tmp, CALIB_PATH)
     return CALIB_PATH
 

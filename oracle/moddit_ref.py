@@ -20,10 +20,21 @@ __all__ = [
     "probability_map", "replay_map", "replay_map_rows", "refresh_merge", "step_phase", "video_layout",
     "cogvideox_grid", "e4m3_decode", "e4m3_encode", "quantize_qkv", "attention_q8",
     "attention_q8_with_bound", "q8_exact_error_bound", "e4m3_flip_candidates",
+    "FP8_MFMA_SUM_REL", "FP8_MFMA_ACC_REL",
     "MODE_SPARSE", "MODE_BLOCK_DIAGONAL", "MODE_FULL",
 ]
 
 MODE_SPARSE, MODE_BLOCK_DIAGONAL, MODE_FULL = 0, 1, 2
+
+# Summation error of one v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3 operands, fp32 C): the
+# instruction does not add its 64 products in exact fp32; its result C_in + sum_k a_k b_k
+# is within FP8_MFMA_SUM_REL * sum_k |a_k b_k| + FP8_MFMA_ACC_REL * |C_in| of the exact
+# value (plus the final fp32 rounding). Characterised on MI355X with the calibration
+# probe moddit_calib_mfma_precision over 11 operand distributions (worst observed 2^-11.5
+# of sum |a b| and, beyond that, 2^-22.2 of |C_in|); tests/test_gpu_calib.py holds the
+# instruction to these constants. The bf16 MFMA sums to fp32 accuracy (2^-23.5).
+FP8_MFMA_SUM_REL = 2.0 ** -10
+FP8_MFMA_ACC_REL = 2.0 ** -21
 
 
 # --------------------------------------------------------------------------------------
@@ -670,7 +681,8 @@ def e4m3_flip_candidates(p: np.ndarray, tol: np.ndarray) -> np.ndarray:
 def attention_q8_with_bound(qz: Dict[str, np.ndarray], token_mask: Optional[np.ndarray] = None,
                             scale: Optional[float] = None, slack: float = 1.5,
                             shift: float = 7.0, origin: int = 0, emulate_fp32: bool = False,
-                            p_jitter: float = 0.0, jitter_seed: int = 0):
+                            p_jitter: float = 0.0, jitter_seed: int = 0,
+                            mfma_jitter: float = 0.0):
     """`attention_q8` plus, per output element, a bound on how far an implementation of
     the same arithmetic in fp32 (the kernel) can be from this fp64 model:
 
@@ -681,6 +693,8 @@ def attention_q8_with_bound(qz: Dict[str, np.ndarray], token_mask: Optional[np.n
       - a row whose lazy-max decision (tile max > m + slack) lies within 4e-6 (1 + |m|)
         of its threshold may move its max at another tile, after which every P of the row
         can round the other way: 2^-3 (1 + 2^-4) sum_j P_j |v8_j| for that row;
+      - the fp8 MFMA's own summation of each tile's 64 products P8 v8 onto the
+        accumulator: FP8_MFMA_SUM_REL sum_tile P8 |v8| + FP8_MFMA_ACC_REL |acc| per tile;
       - fp32 accumulation of O and of the row sum l: (keys + 2 tiles + 256) 2^-24
         relative to |O| + sum_j P_j |v8_j| v_scale / l (recursive-summation bound);
       - the kernel's bf16 output rounding: 2^-9 of |O| plus the terms above, taken as
@@ -690,13 +704,15 @@ def attention_q8_with_bound(qz: Dict[str, np.ndarray], token_mask: Optional[np.n
     arithmetic, used on the CPU to exercise the bound); p_jitter: multiply every P by
     1 + p_jitter * U(-1, 1) (seeded) before it is rounded and summed (another rendering
     whose P differ by up to p_jitter, for the same purpose; the bound itself is computed
-    from the unperturbed model). Returns (O, LSE, bound)."""
+    from the unperturbed model); mfma_jitter: add mfma_jitter * U(-1, 1) times the fp8
+    MFMA error model's allowance to each tile's P.V sum (a rendering whose MFMA sums err
+    by up to mfma_jitter of what the model allows). Returns (O, LSE, bound)."""
     return _attention_q8_core(qz, token_mask, scale, slack, shift, origin, True, emulate_fp32,
-                              p_jitter, jitter_seed)
+                              p_jitter, jitter_seed, mfma_jitter)
 
 
 def _attention_q8_core(qz, token_mask, scale, slack, shift, origin, want_bound, fp32,
-                       p_jitter=0.0, jitter_seed=0):
+                       p_jitter=0.0, jitter_seed=0, mfma_jitter=0.0):
     q8 = qz["q8"].astype(np.float64)
     k8 = qz["k8"].astype(np.float64)
     H, S, D = q8.shape
@@ -729,6 +745,7 @@ def _attention_q8_core(qz, token_mask, scale, slack, shift, origin, want_bound, 
         if want_bound:
             flip_acc = np.zeros((S, D))
             tot_acc = np.zeros((S, D))
+            mfma_acc = np.zeros((S, D))
             near_max = np.zeros(S, bool)
             n_keys = np.zeros(S)
             n_tiles = np.zeros(S)
@@ -755,9 +772,15 @@ def _attention_q8_core(qz, token_mask, scale, slack, shift, origin, want_bound, 
             if p_jitter:
                 p = p * (1 + p_jitter * jrng.uniform(-1, 1, p.shape))
             p8 = e4m3_decode(e4m3_encode(p))
-            acc = acc * alpha[:, None] + p8 @ v[h, k0:k1]
+            acc_in = acc * alpha[:, None]
+            mfma_allow = (FP8_MFMA_SUM_REL * (p8 @ av[k0:k1])
+                          + FP8_MFMA_ACC_REL * np.abs(acc_in)) if (want_bound or mfma_jitter) else 0
+            acc = acc_in + p8 @ v[h, k0:k1]
+            if mfma_jitter:
+                acc = acc + mfma_jitter * jrng.uniform(-1, 1, acc.shape) * mfma_allow
             l = l * alpha + p.sum(axis=1)
             if want_bound:
+                mfma_acc = mfma_acc * alpha[:, None] + mfma_allow
                 p = p_model
                 keyed = np.isfinite(st)
                 tol = 4e-6 * (1 + np.abs(np.where(keyed, st, 0)))
@@ -779,7 +802,8 @@ def _attention_q8_core(qz, token_mask, scale, slack, shift, origin, want_bound, 
             flip_o = np.where(near_max[:, None], 2.0 ** -3 * (1 + 2.0 ** -4) * tot,
                               flip_acc * vs[h][None, :] * linv)
             gam = (n_keys + 2 * n_tiles + 256)[:, None] * 2.0 ** -24
-            terms = flip_o + gam * (np.abs(out[h]) + tot)
+            mfma_o = mfma_acc * vs[h][None, :] * linv
+            terms = flip_o + mfma_o + gam * (np.abs(out[h]) + tot)
             bound[h] = terms * (1 + 2.0 ** -8) + 2.0 ** -8 * np.abs(out[h])
     return out, lse, bound
 
@@ -806,11 +830,14 @@ def q8_exact_error_bound(q, k, v, q8, q_scale, k8, k_scale, k_mean, v_scale,
         error instead: V below 2^-6 v_scale: 2^-10 v_scale (twice, both factors); P below
         2^-6: 2^-10 (1 + 2^-4) |v_j| / l with l >= 2^7 (P = 2^(y - m + 7), the lazy max
         m <= the row max y_max), for keys with y_j < y_max - 13 (log2 units) only;
-      - fp32 accumulation (O and l over the keys): (keys + 2 tiles + 256) 2^-24 relative
-        to |o| + 2 e^2E sum_j w_j |v_j|;
+      - the fp8 MFMA's summation (FP8_MFMA_SUM_REL of each tile's sum |P8 v8| and
+        FP8_MFMA_ACC_REL of the accumulator per tile, which is at most the whole row's
+        sum): (FP8_MFMA_SUM_REL + tiles FP8_MFMA_ACC_REL) (1 + 2^-4) e^2E sum_j w_j |v_j|;
+      - fp32 accumulation (O and l over the keys): (keys + 2 tiles + 256) 2^-24
+        relative to |o| + 2 e^2E sum_j w_j |v_j|;
       - bf16 output rounding: 2^-9 of |o| plus all the above.
-    drop: names of terms to leave out ("score", "e4m3", "subnormal", "accumulation",
-    "output"), for tests that show each one is needed.
+    drop: names of terms to leave out ("score", "e4m3", "subnormal", "mfma",
+    "accumulation", "output"), for tests that show each one is needed.
     Returns (o (R, D), bound (R, D), E (R,))."""
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
@@ -847,11 +874,14 @@ def q8_exact_error_bound(q, k, v, q8, q_scale, k8, k_scale, k_mean, v_scale,
     vsc = np.asarray(v_scale, np.float64)[None, :]
     grow = np.exp(2 * E)[:, None]
     on = {t: 0.0 if t in drop else 1.0
-          for t in ("score", "e4m3", "subnormal", "accumulation", "output")}
+          for t in ("score", "e4m3", "subnormal", "mfma", "accumulation", "output")}
+    tiles = ((keys + 63) // 64)[:, None]
     pre = (on["score"] * (grow - 1) * bv
            + on["e4m3"] * grow * (2.0 ** -3 + 2.0 ** -8) * bv
            + on["subnormal"] * (grow * 2.0 ** -9 * vsc
                                 + 2.0 ** -17 * (1 + 2.0 ** -4) * (sub_v + n_sub * vsc * 2.0 ** -10))
+           + on["mfma"] * (FP8_MFMA_SUM_REL + tiles * FP8_MFMA_ACC_REL) * (1 + 2.0 ** -4)
+           * grow * bv
            + on["accumulation"] * gam * (np.abs(o) + 2 * grow * bv))
     out_r = on["output"] * 2.0 ** -9
     bound = np.where(has[:, None], pre * (1 + out_r) + out_r * np.abs(o), 0.0)

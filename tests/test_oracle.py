@@ -585,6 +585,13 @@ def test_q8_model_bound_covers_fp32_renderings_and_catches_larger_errors(case):
     assert np.all(np.abs(oj - o) <= b)
     ob, _, _ = O.attention_q8_with_bound(z, tm, origin=origin, p_jitter=1e-3, jitter_seed=case)
     assert (np.abs(ob - o) > b).sum() > 0
+    # fp8 MFMA sums that err by up to the instruction's characterised allowance stay
+    # inside; eight times that allowance does not
+    om, _, _ = O.attention_q8_with_bound(z, tm, origin=origin, mfma_jitter=1.0, jitter_seed=case)
+    assert np.all(np.abs(om - o) <= b)
+    om8, _, _ = O.attention_q8_with_bound(z, tm, origin=origin, mfma_jitter=8.0,
+                                          jitter_seed=case)
+    assert (np.abs(om8 - o) > b).sum() > 0
 
 
 def _exact_bound(q, k, v, z, tm, origin=0, drop=()):
@@ -612,6 +619,12 @@ def test_q8_exact_bound_holds_for_the_modelled_arithmetic(case):
     r = np.abs(o8 - o) / b
     assert r.max() <= 1.0 and r.max() > 0.05, r.max()
     assert np.all(E >= 0)
+    # renderings with fp32 scores and exp2, and with fp8 MFMA sums erring by the
+    # instruction's characterised allowance, stay inside too
+    for kw in (dict(emulate_fp32=True), dict(mfma_jitter=1.0, jitter_seed=case)):
+        o2 = O.attention_q8_with_bound(z, tm, origin=origin, **kw)[0][0]
+        o2 = O.bf16_round(o2.astype(np.float32)).astype(np.float64)
+        assert np.all(np.abs(o2 - o) <= b), kw
 
 
 def test_q8_exact_bound_needs_each_rounding_term():
