@@ -18,8 +18,9 @@ Under "vendor": torch's own scaled_dot_product_attention (flash backend) on the 
 layer's dense attention, and a hipBLASLt bf16 GEMM with its board power and clock.
 Under "other_configs", after the headline's timed region: the headline mask executed
 with union tile rows (the reference engine's 128-row granularity), the 50-step
-denoising trajectory on the headline layer and the Wan-like layer
-(configs[2]), each in compact form.
+denoising trajectory on the headline layer, the Wan-like layer
+(configs[2]), the CogVideoX-like layer and the plumbing shape,
+each in compact form.
 
     python bench.py [--steps K] [--warmup W] [--tile-rows union|exact] [--no-cpu] [--no-q8]
                     [--no-extra]
@@ -832,7 +833,7 @@ def main(argv=None):
     ap.add_argument("--no-q8", action="store_true", help="skip the int8/fp8 path's timings")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the compact legs of the default run (union rows, the 50-step "
-                         "trajectory, the Wan-like layer)")
+                         "trajectory, the Wan-like, CogVideoX-like and plumbing layers)")
     ap.add_argument("--precision", choices=("bf16", "int8"), default="bf16",
                     help="--sweep only: arithmetic of the sparse steps (the headline line is bf16)")
     ap.add_argument("--sweep", action="store_true",
@@ -1063,6 +1064,18 @@ def main(argv=None):
                                              threshold=args.threshold)
         log("Wan-like layer")
         extra["wan"] = layer_leg("wan", reps=args.steps, threshold=args.threshold)
+        for name in ("cogvideox", "plumbing"):
+            log(f"{name} configuration")
+            r = run_mask_config(name, steps=args.steps, warmup=args.warmup, no_cpu=True)
+            extra[name] = {"workload": r["config"]["workload"],
+                           "mask_sparsity": r["config"]["mask_sparsity"],
+                           "sparse_ms": r["ms_per_step"], "dense_ms": r["dense_ms"],
+                           "effective_tflops": r["value"],
+                           "executed_tflops": r["executed_tflops"],
+                           "frac": round(r["executed_tflops"] / MI355X_BF16_DENSE_TFLOPS, 4),
+                           "speedup_vs_dense": r["speedup_vs_dense"],
+                           "mask_overhead_ms": r["mask_overhead_ms"]}
+            torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
