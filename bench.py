@@ -394,6 +394,10 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
                 hi = mid - 1
         topk_for[tgt] = best[0]
 
+    def refresh_state(prev_maps):
+        return {"block_size": bs, "threshold": threshold, "model_type": "wan",
+                "video_token_num": N, "text_token_num": 0, "prev_full_maps": prev_maps}
+
     out = torch.empty_like(q)
     stream = torch.cuda.current_stream()
     rows = []
@@ -413,10 +417,14 @@ def run_sweep(q, k, v, art, *, H, N, D, bpf, bs, union, threshold, config, steps
             e[1].record(stream)
             e[2].record(stream)
         elif ph in ("map_fit", "map_fit_predict", "refresh"):
-            _, cur_map = md.flash_attn_with_sparsity_map(q, k, v, threshold, bs, model_type="wan")
-            cur_map = cur_map[0]
             if ph == "refresh":
-                cur_map = ops.refresh_merge(smap, cur_map, mask)
+                # the step machine's refresh: dense pass + the map replayed at the mask's
+                # active blocks into a copy of the previous map (the merged map)
+                _, cur_map = md.attn_mask._refresh_map_step(q, k, v, refresh_state(smap), mask)
+            else:
+                _, cur_map = md.flash_attn_with_sparsity_map(q, k, v, threshold, bs,
+                                                             model_type="wan")
+                cur_map = cur_map[0]
             e[1].record(stream)
             if ph != "map_fit":
                 x_new = md.lstsq.fit(ops.compute_mts(cur_map, bpf), n, bpf, 1.0)
@@ -1030,6 +1038,15 @@ def main(argv=None):
                                               q_video_offset=0, k_video_offset=0,
                                               video_blocks=N // bs, block_size=bs), 2)
     replay_ms = min(rp)
+    # a refresh step's replay: only the current mask's active blocks, merged into the map
+    tiles_v = ops.mask_to_tiles(art["mask"], bs, union_rows=False)
+    merged = art["smap"].clone()
+    rm = time_events(lambda: ops.sparsity_map_merge(
+        q, k, lse, tiles_v, merged.unsqueeze(0), softmax_scale=D ** -0.5,
+        log_threshold=math.log(args.threshold), q_video_offset=0, k_video_offset=0,
+        video_blocks=N // bs, block_size=bs), 3)
+    refresh_replay_ms = min(rm)
+    del merged
     replay_board_ms, replay_board = sampled_loop(
         lambda: ops.sparsity_map(q, k, lse, softmax_scale=D ** -0.5,
                                  log_threshold=math.log(args.threshold), q_video_offset=0,
@@ -1138,6 +1155,8 @@ def main(argv=None):
         "replay_ms": round(replay_ms, 3),
         "replay_board": replay_board,
         "map_step_ms": round(dense_ms + replay_ms, 3),
+        "refresh_replay_ms": round(refresh_replay_ms, 3),
+        "refresh_step_ms": round(dense_ms + refresh_replay_ms, 3),
         "map_step_fused_ms": round(map_step_fused_ms, 3),
         "mask_overhead_amortized_ms": round(overhead_ms + replay_ms / 10.0, 4),
         "speedup_incl_mask": round(dense_ms / (ms + overhead_ms), 3),

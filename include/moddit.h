@@ -189,6 +189,27 @@ int moddit_sparsity_map(const void* q, const void* k, const float* lse, void* ma
                         int dtype, moddit_stream_t stream);
 
 /*
+ * The refresh step's map update in one pass: the cells of moddit_sparsity_map listed in
+ * tile lists (counts, entries: the moddit_mask_to_tiles format with exact rows, over the
+ * video x video block mask: n_qtiles = ceil(video_blocks * block_size / 128) query tiles
+ * of 128 rows, entries key_tile << 2 | row bits; with block_size 128 each active block
+ * column j is the entry pair 2j, 2j+1 with both row bits) are computed as
+ * moddit_sparsity_map computes them and written into map_inout; every other cell keeps
+ * its value. With map_inout holding the previous map and the lists those of the current
+ * mask, the result is the merged map of the refresh step,
+ * where(mask == False, prev, current) (MoD/mod/attn_mask.py:659-675 over
+ * flash_attn_with_sparsity_map, MoD/mod/triton_flash_sparsity.py:274-341), bit for bit,
+ * at the cost of the active cells only.
+ */
+int moddit_sparsity_map_merge(const void* q, const void* k, const float* lse, void* map_inout,
+                              int batch, int heads, int seq_len, int head_dim,
+                              const int64_t q_strides[3], const int64_t k_strides[3],
+                              float softmax_scale, float log_threshold, int q_video_offset,
+                              int k_video_offset, int video_blocks, int block_size, int dtype,
+                              const int32_t* tile_counts, const int32_t* tile_entries,
+                              int n_qtiles, int cap, moddit_stream_t stream);
+
+/*
  * M^T S for the line model, per head (H, 3n) fp32:
  *   [0, 2n-1)   diagonal sums, index k <-> offset k-(n-1) (col - row)
  *   [2n-1, 3n-1) column sums

@@ -46,6 +46,8 @@ _SIGNATURES = {
                                         _i, _i, _c_i64p, _f, _i, _vp, _vp, _i, _i, _i, _vp]),
     "moddit_sparsity_map": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _c_i64p, _c_i64p,
                                  _f, _f, _i, _i, _i, _i, _i, _vp]),
+    "moddit_sparsity_map_merge": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _c_i64p, _c_i64p,
+                                       _f, _f, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp]),
     "moddit_mts": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "moddit_mts_workspace_bytes": (ctypes.c_int64, [_i, _i]),
     "moddit_mtm_host": (_i, [_i, _i, ctypes.c_double, _vp]),

@@ -20,6 +20,9 @@ Differences that are deliberate:
     index;
   * the mask kernel also emits the attention tile lists, so sparse steps do not
     convert the mask again;
+  * refresh steps replay the sparsity map only at the blocks the current mask keeps
+    and write them into a copy of the previous map: the reference's full replay followed
+    by where(mask == False, prev, current) gives the same map, bit for bit;
   * sparse types other than 'mod-dit' ('radial', 'spargeattn') call third-party kernels
     in the reference and raise NotImplementedError here;
   * the engine's arithmetic is bf16 by default; the state key 'precision' = 'int8'
@@ -34,7 +37,8 @@ from typing import Dict, List, Optional, Tuple
 import torch
 
 from . import _lib, ops
-from .flash_sparsity import flash_attn_with_sparsity_map, padded_grid
+from .flash_sparsity import (_validate_inputs, flash_attn_with_sparsity_map, log_threshold,
+                             padded_grid)
 from .lstsq import solve_lstsq
 from .state import is_warmup_complete
 
@@ -381,6 +385,27 @@ def _video_part(warmup_state: Dict, mask: torch.Tensor) -> torch.Tensor:
     return mask
 
 
+def _refresh_map_step(query, key, value, warmup_state: Dict, current_mask: torch.Tensor):
+    """Dense attention and the merged map of a refresh step (MoD/mod/attn_mask.py:659-675).
+
+    The reference computes the whole map with flash_attn_with_sparsity_map and keeps it
+    only where the current (video) mask is True: where(mask == False, prev, current).
+    Here the replay runs over the mask's active blocks only, writing them into a copy of
+    the previous map; the result is the same map, bit for bit."""
+    bs = warmup_state["block_size"]
+    thr, video_blocks, q_off, k_off = _validate_inputs(
+        query, key, value, warmup_state["threshold"], bs, warmup_state["model_type"],
+        warmup_state["video_token_num"], warmup_state["text_token_num"])
+    sm_scale = query.shape[-1] ** -0.5
+    out, lse = ops.flash_fwd(query, key, value, softmax_scale=sm_scale, return_lse=True)
+    tiles = ops.mask_to_tiles(current_mask, bs, union_rows=False)
+    merged = warmup_state["prev_full_maps"].clone(memory_format=torch.contiguous_format)
+    ops.sparsity_map_merge(query, key, lse, tiles, merged.unsqueeze(0), softmax_scale=sm_scale,
+                           log_threshold=log_threshold(thr), q_video_offset=q_off,
+                           k_video_offset=k_off, video_blocks=video_blocks, block_size=bs)
+    return out, merged
+
+
 def SparseAttentionWithMap(
     query: torch.Tensor,
     key: torch.Tensor,
@@ -438,15 +463,9 @@ def SparseAttentionWithMap(
         raise RuntimeError("SparseAttentionWithMap: no mask was predicted during warmup")
     T = warmup_state["predict_T"]
     if (current_step - W) % T == T - 1:
-        output, current_sparse_map = flash_attn_with_sparsity_map(
-            query, key, value, threshold=warmup_state["threshold"],
-            block_size=warmup_state["block_size"], model_type=warmup_state["model_type"],
-            video_token_num=warmup_state["video_token_num"],
-            text_token_num=warmup_state["text_token_num"])
-        current_sparse_map = current_sparse_map.squeeze(0)
         current_mask = _video_part(warmup_state, warmup_state["mask"])
-        warmup_state["prev_full_maps"] = ops.refresh_merge(
-            warmup_state["prev_full_maps"], current_sparse_map, current_mask)
+        output, warmup_state["prev_full_maps"] = _refresh_map_step(
+            query, key, value, warmup_state, current_mask)
         features = extract_attention_features(
             warmup_state=warmup_state, S_T=warmup_state["prev_full_maps"], layer_idx=layer_idx,
             blocks_per_frame=warmup_state["blocks_per_frame"], use_cuda=warmup_state["use_cuda"])

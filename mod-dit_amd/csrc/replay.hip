@@ -16,6 +16,11 @@
 // register staging it needs no more cycles. Its maps match the 32x32x16 form's
 // bit for bit on the tested layers (both accumulate the same products in fp32).
 //
+// The list mode (kList) replays only the (query block, key tile) pairs of per-(head, 128-row
+// query tile) key-tile lists with row bits, the format of moddit_mask_to_tiles, and
+// writes only those cells: the refresh step's merge (MoD/mod/attn_mask.py:663-675) keeps
+// the new map only where the current mask is active, so the other cells need no replay.
+//
 // Reference semantics: flash_sparsity_replay_kernel
 // (MoD/mod/cuda_flash_sparsity_kernel.cu:41-169): Q scaled in fp32 and rounded to the
 // input dtype (:86-92), fp32 products, strict '<' against lse + log_threshold (:138-143),
@@ -67,9 +72,13 @@ struct ReplayParams {
   float scale;
   float log_thr;
   uint32_t k_bytes;  // byte span of one head's video K rows
+  // list mode: entries[h][qt][i] = key_tile << 2 | row bits, i < counts[h][qt]
+  const int32_t* counts;
+  const int32_t* entries;
+  int cap;
 };
 
-template <int D, typename E, bool kRagged>
+template <int D, typename E, bool kRagged, bool kList>
 __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p) {
   using L = ReplayLds<D>;
   using V8 = typename E::vec8;
@@ -158,20 +167,49 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
   for (int c = 0; c < kDC; ++c)
     k_rd[c] = static_cast<uint32_t>(c16 * L::kRowBytes + (((4 * c + g) ^ replay_swz<D>(c16)) * 16));
 
-  dma_tile(0, 0);
+  // The key tiles to sweep: all of them, or (list mode) the entries of this query tile.
+  // A list entry outside [0, n_ktiles) holds no key of the video region: it is executed
+  // by no wave and written nowhere (its DMA loads tile 0).
+  int n_iter = p.n_ktiles;
+  const int32_t* list = nullptr;
+  if constexpr (kList) {
+    const int64_t slot = static_cast<int64_t>(h) * p.n_qtiles + qt;
+    n_iter = p.counts[slot];
+    n_iter = n_iter < 0 ? 0 : (n_iter < p.cap ? n_iter : p.cap);
+    list = p.entries + slot * p.cap;
+  }
+  const int wbit = 1 << (wave >> 1);  // row bit of this wave's 64 rows (list mode)
+  auto key_tile = [&](int i, int& flags) -> int {
+    if constexpr (!kList) {
+      flags = 3;
+      return i;
+    } else {
+      const int e = __builtin_amdgcn_readfirstlane(list[i]);
+      const int kt = e >> 2;
+      const bool in = kt >= 0 && kt < p.n_ktiles;
+      flags = in ? (e & 3) : 0;
+      return in ? kt : 0;
+    }
+  };
+
+  int flags_cur = 0;
+  int kt_cur = n_iter > 0 ? key_tile(0, flags_cur) : 0;
+  if (n_iter > 0) dma_tile(kt_cur, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   const float inv_area = 1.0f / static_cast<float>(p.block * p.block);
   uint16_t* out_bh = p.out + static_cast<int64_t>(bh) * p.nblk * p.nblk;
 
-  for (int it = 0; it < p.n_ktiles; ++it) {
-    const bool has_next = it + 1 < p.n_ktiles;
+  for (int it = 0; it < n_iter; ++it) {
+    const bool has_next = it + 1 < n_iter;
+    int flags_next = 0;
+    const int kt_next = has_next ? key_tile(it + 1, flags_next) : 0;
     // the stage of tile it+1 held tile it-1, which every wave finished reading before
     // the previous iteration's barrier
-    if (has_next) dma_tile(it + 1, (it + 1) & 1);
+    if (has_next) dma_tile(kt_next, (it + 1) & 1);
 
-    if (wave_active) {
+    if (wave_active && (flags_cur & wbit)) {
       const unsigned char* ks = smem + (it & 1) * L::kKBytes;
       // s[kb][qq]: keys 16kb + 4g + j of query vrow0 + 16qq + c16
       f32x4 s[4][2];
@@ -187,9 +225,9 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
         }
       }
       int total = 0;
-      if (kRagged && it * kBN + kBN > p.valid_k) {
+      if (kRagged && kt_cur * kBN + kBN > p.valid_k) {
         // keys at or past the sequence end are not counted
-        const int key0 = it * kBN + 4 * g;
+        const int key0 = kt_cur * kBN + 4 * g;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -216,7 +254,47 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
     __syncthreads();
 
     const int slot_hi = it % kFlush;
-    if (slot_hi == kFlush - 1 || !has_next) {
+    if (kList && (slot_hi == kFlush - 1 || !has_next)) {
+      // list mode: position s of the flush holds the entry it - slot_hi + s
+      const int it0 = it - slot_hi;
+      const int hb = ((it / kFlush) & 1) * kFlush;
+      if (p.block == 64) {
+        if (tid < 2 * kFlush) {
+          const int qsub = tid / kFlush;
+          const int s = tid % kFlush;
+          const int qblk = 2 * qt + qsub;
+          if (s <= slot_hi && qblk < p.nblk) {
+            const int e = list[it0 + s];
+            const int kt = e >> 2;
+            if (((e >> qsub) & 1) && kt >= 0 && kt < p.n_ktiles) {
+              const int c = cnt[(2 * qsub) * 2 * kFlush + hb + s] +
+                            cnt[(2 * qsub + 1) * 2 * kFlush + hb + s];
+              const float ratio = static_cast<float>(c) * inv_area;
+              out_bh[static_cast<int64_t>(qblk) * p.nblk + kt] = Fp16::from_float(ratio);
+            }
+          }
+        }
+      } else {
+        // one 128-row block per query tile; the entries come in pairs (2j, 2j+1), both
+        // rows bits set, one pair per active key block j (the moddit_mask_to_tiles list
+        // of a 128-token block mask), so a pair never straddles a flush (kFlush is even)
+        if (tid < kFlush / 2) {
+          const int u = tid;
+          if (2 * u + 1 <= slot_hi) {
+            const int e = list[it0 + 2 * u];
+            const int kt = e >> 2;
+            if ((e & 3) == 3 && kt >= 0 && kt + 1 < p.n_ktiles) {
+              int c = 0;
+#pragma unroll
+              for (int w = 0; w < 4; ++w)
+                c += cnt[w * 2 * kFlush + hb + 2 * u] + cnt[w * 2 * kFlush + hb + 2 * u + 1];
+              const float ratio = static_cast<float>(c) * inv_area;
+              out_bh[static_cast<int64_t>(qt) * p.nblk + kt / 2] = Fp16::from_float(ratio);
+            }
+          }
+        }
+      }
+    } else if (!kList && (slot_hi == kFlush - 1 || !has_next)) {
       const int it0 = it - slot_hi;  // first key tile of this flush
       const int hb = ((it / kFlush) & 1) * kFlush;  // ring half it was written to
       if (p.block == 64) {
@@ -246,13 +324,15 @@ __global__ __launch_bounds__(kThreads, 2) void replay_map_kernel(ReplayParams p)
         }
       }
     }
+    kt_cur = kt_next;
+    flags_cur = flags_next;
   }
 }
 
-template <int D, typename E, bool kRagged>
+template <int D, typename E, bool kRagged, bool kList>
 int launch_replay_impl(const ReplayParams& p, int batch, hipStream_t stream) {
   using L = ReplayLds<D>;
-  auto kernel = replay_map_kernel<D, E, kRagged>;
+  auto kernel = replay_map_kernel<D, E, kRagged, kList>;
   static LaunchSetup once;
   if (set_dynamic_lds_once(once, reinterpret_cast<const void*>(kernel), L::kTotal) != hipSuccess) {
     set_error("sparsity_map: cannot reserve %d bytes of LDS", L::kTotal);
@@ -272,21 +352,27 @@ int launch_replay_impl(const ReplayParams& p, int batch, hipStream_t stream) {
 
 template <int D, typename E>
 int launch_replay(const ReplayParams& p, int batch, hipStream_t stream) {
-  if (p.valid_k == p.n_ktiles * kBN) return launch_replay_impl<D, E, false>(p, batch, stream);
-  return launch_replay_impl<D, E, true>(p, batch, stream);
+  const bool aligned = p.valid_k == p.n_ktiles * kBN;
+  if (p.entries != nullptr)
+    return aligned ? launch_replay_impl<D, E, false, true>(p, batch, stream)
+                   : launch_replay_impl<D, E, true, true>(p, batch, stream);
+  return aligned ? launch_replay_impl<D, E, false, false>(p, batch, stream)
+                 : launch_replay_impl<D, E, true, false>(p, batch, stream);
 }
 
 }  // namespace
 }  // namespace moddit
 
-extern "C" int moddit_sparsity_map(const void* q, const void* k, const float* lse, void* map_out,
-                                   int batch, int heads, int seq_len, int head_dim,
-                                   const int64_t q_strides[3], const int64_t k_strides[3],
-                                   float softmax_scale, float log_threshold, int q_video_offset,
-                                   int k_video_offset, int video_blocks, int block_size,
-                                   int dtype, moddit_stream_t stream) {
-  using namespace moddit;
-  clear_error();
+namespace moddit {
+namespace {
+
+int sparsity_map_common(const void* q, const void* k, const float* lse, void* map_out,
+                        int batch, int heads, int seq_len, int head_dim,
+                        const int64_t q_strides[3], const int64_t k_strides[3],
+                        float softmax_scale, float log_threshold, int q_video_offset,
+                        int k_video_offset, int video_blocks, int block_size, int dtype,
+                        const int32_t* tile_counts, const int32_t* tile_entries, int n_qtiles,
+                        int cap, moddit_stream_t stream) {
   MODDIT_CHECK_ARG(q && k && lse && map_out && q_strides && k_strides,
                    "sparsity_map: null pointer argument");
   if (head_dim != 64 && head_dim != 128) {
@@ -336,6 +422,16 @@ extern "C" int moddit_sparsity_map(const void* q, const void* k, const float* ls
   p.xcd_run = xcd_run_for(vt * head_dim * 2);  // the video K rows a sweep reads
   p.scale = softmax_scale;
   p.log_thr = log_threshold;
+  p.counts = tile_counts;
+  p.entries = tile_entries;
+  p.cap = cap;
+  if (tile_entries != nullptr) {
+    MODDIT_CHECK_ARG(tile_counts != nullptr, "sparsity_map_merge: null tile counts");
+    MODDIT_CHECK_ARG(n_qtiles == p.n_qtiles,
+                     "sparsity_map_merge: the tile lists have %d query tiles, the video region "
+                     "needs %d", n_qtiles, p.n_qtiles);
+    MODDIT_CHECK_ARG(cap >= 0, "sparsity_map_merge: negative list capacity");
+  }
   const int64_t k_span = (static_cast<int64_t>(p.valid_k) - 1) * k_strides[2] * 2 + head_dim * 2;
   const int64_t k_grid = vt * k_strides[2] * 2;  // largest offset a (ragged) tile forms
   if (k_span > 0x7fffffffLL || k_grid > 0x7fffffffLL) {
@@ -349,4 +445,37 @@ extern "C" int moddit_sparsity_map(const void* q, const void* k, const float* ls
   if (head_dim == 128)
     return bf ? launch_replay<128, Bf16>(p, batch, st) : launch_replay<128, Fp16>(p, batch, st);
   return bf ? launch_replay<64, Bf16>(p, batch, st) : launch_replay<64, Fp16>(p, batch, st);
+}
+
+}  // namespace
+}  // namespace moddit
+
+extern "C" int moddit_sparsity_map(const void* q, const void* k, const float* lse, void* map_out,
+                                   int batch, int heads, int seq_len, int head_dim,
+                                   const int64_t q_strides[3], const int64_t k_strides[3],
+                                   float softmax_scale, float log_threshold, int q_video_offset,
+                                   int k_video_offset, int video_blocks, int block_size,
+                                   int dtype, moddit_stream_t stream) {
+  moddit::clear_error();
+  return moddit::sparsity_map_common(q, k, lse, map_out, batch, heads, seq_len, head_dim,
+                                     q_strides, k_strides, softmax_scale, log_threshold,
+                                     q_video_offset, k_video_offset, video_blocks, block_size,
+                                     dtype, nullptr, nullptr, 0, 0, stream);
+}
+
+extern "C" int moddit_sparsity_map_merge(const void* q, const void* k, const float* lse,
+                                         void* map_inout, int batch, int heads, int seq_len,
+                                         int head_dim, const int64_t q_strides[3],
+                                         const int64_t k_strides[3], float softmax_scale,
+                                         float log_threshold, int q_video_offset,
+                                         int k_video_offset, int video_blocks, int block_size,
+                                         int dtype, const int32_t* tile_counts,
+                                         const int32_t* tile_entries, int n_qtiles, int cap,
+                                         moddit_stream_t stream) {
+  moddit::clear_error();
+  MODDIT_CHECK_ARG(tile_counts && tile_entries, "sparsity_map_merge: null tile lists");
+  return moddit::sparsity_map_common(q, k, lse, map_inout, batch, heads, seq_len, head_dim,
+                                     q_strides, k_strides, softmax_scale, log_threshold,
+                                     q_video_offset, k_video_offset, video_blocks, block_size,
+                                     dtype, tile_counts, tile_entries, n_qtiles, cap, stream);
 }

@@ -298,6 +298,43 @@ def sparsity_map(query, key, lse, *, softmax_scale, log_threshold, q_video_offse
     return out
 
 
+def sparsity_map_merge(query, key, lse, tiles: TileList, map_inout, *, softmax_scale,
+                       log_threshold, q_video_offset, k_video_offset, video_blocks, block_size):
+    """Write the sparsity_map cells that `tiles` (exact rows, over the video block mask)
+    list into `map_inout` (B,H,n,n) fp16 contiguous, in place; the other cells keep their
+    values (the refresh step's merge at the cost of the active cells)."""
+    _require_gpu(query, key, lse, map_inout, what="sparsity_map_merge")
+    if query.ndim != 4 or key.ndim != 4 or query.shape != key.shape:
+        raise RuntimeError("Q and K must have identical shape [B, H, S, D]")
+    if lse.ndim != 3 or tuple(lse.shape) != tuple(query.shape[:3]):
+        raise RuntimeError("LSE shape must match Q except for head_dim")
+    if lse.dtype != torch.float32:
+        raise RuntimeError("LSE must be float32")
+    if query.dtype != key.dtype:
+        raise RuntimeError("Q and K dtypes must match")
+    B, H, S, D = query.shape
+    if (map_inout.dtype != torch.float16 or not map_inout.is_contiguous()
+            or tuple(map_inout.shape) != (B, H, video_blocks, video_blocks)):
+        raise ValueError(f"map must be a contiguous fp16 tensor of shape "
+                         f"{(B, H, video_blocks, video_blocks)}")
+    if tiles.union_rows or tiles.block_size != block_size or tiles.origin != 0:
+        raise ValueError("the merge needs exact-row tile lists of the video block mask at the "
+                         "map's block size")
+    if tiles.counts.shape[0] != H:
+        raise ValueError(f"tile lists cover {tiles.counts.shape[0]} heads, the map has {H}")
+    dt = _attn_dtype(query)
+    query, key = _attn_view(query), _attn_view(key)
+    lse = lse.contiguous()
+    lib = _lib.load()
+    check(lib.moddit_sparsity_map_merge(
+        query.data_ptr(), key.data_ptr(), lse.data_ptr(), map_inout.data_ptr(), B, H, S, D,
+        strides3(*query.stride()[:3]), strides3(*key.stride()[:3]), float(softmax_scale),
+        float(log_threshold), int(q_video_offset), int(k_video_offset), int(video_blocks),
+        int(block_size), dt, tiles.counts.data_ptr(), tiles.entries.data_ptr(),
+        tiles.n_qtiles, tiles.cap, _stream(query)), "moddit_sparsity_map_merge")
+    return map_inout
+
+
 # --------------------------------------------------------------------------------------
 # least squares
 # --------------------------------------------------------------------------------------

@@ -222,6 +222,43 @@ def test_random_replay_map_bit_exact(i):
         assert np.array_equal(got[b].cpu().numpy(), ref), (tag, b)
 
 
+@pytest.mark.parametrize("i", range(10))
+def test_random_merged_replay_equals_full_replay_then_merge(i):
+    """The refresh step's map (MoD/mod/attn_mask.py:659-675): the replay run only at the
+    mask's active blocks and written into the previous map equals the full replay merged
+    with where(mask == False, prev, full), bit for bit, for the three layouts, both block
+    sizes, batches of one or two, and masks from empty (case 0) to all-True (case 1)."""
+    import math
+
+    c = _draw_map(300 + i)
+    D, bs, B, H = c["D"], c["bs"], c["B"], c["H"]
+    q = torch.from_numpy(c["qn"]).to(c["dtype"]).to(DEV)
+    k = torch.from_numpy(c["kn"]).to(c["dtype"]).to(DEV)
+    scale = D ** -0.5
+    vb, qo, ko = O.video_layout(c["model_type"], c["S"], c["video"], c["text"], bs)
+    rng = np.random.default_rng(500 + i)
+    density = 0.0 if i == 0 else (1.0 if i == 1 else float(rng.uniform(0.05, 0.6)))
+    mask = rng.random((H, vb, vb)) < density
+    tag = (f"case {i}: {c['model_type']} bs={bs} D={D} {c['dtype']} text={c['text']} "
+           f"video={c['video']} B={B} H={H} density={mask.mean():.2f}")
+    print(tag, flush=True)
+    lse = torch.randn((B, H, c["S"]), generator=torch.Generator().manual_seed(i)).to(DEV)
+    ln_thr = math.log(c["thr"])
+    kw = dict(softmax_scale=scale, log_threshold=ln_thr, q_video_offset=qo, k_video_offset=ko,
+              video_blocks=vb, block_size=bs)
+    full = ops.sparsity_map(q, k, lse, **kw)
+    prev = torch.rand((B, H, vb, vb), generator=torch.Generator().manual_seed(50 + i))
+    prev = prev.to(torch.float16).to(DEV)
+    tiles = ops.mask_to_tiles(torch.from_numpy(mask).to(DEV), bs, union_rows=False)
+    merged = prev.clone()
+    ops.sparsity_map_merge(q, k, lse, tiles, merged, **kw)
+    want = torch.where(torch.from_numpy(mask).to(DEV)[None], full, prev)
+    assert torch.equal(merged, want), tag
+    for b in range(B):
+        ref = O.refresh_merge(prev[b].cpu().numpy(), full[b].cpu().numpy(), mask)
+        assert np.array_equal(merged[b].cpu().numpy(), ref), (tag, b)
+
+
 @pytest.mark.parametrize("i", range(6))
 def test_random_fused_map_pass_equals_two_kernels(i):
     """The fused dense + map kernel: the map equals the separate replay of its own LSE."""

@@ -94,6 +94,13 @@ def test_c_abi_rejects_bad_arguments_before_any_launch():
     assert rc == _lib.MODDIT_EUNSUPPORTED and b"head_dim" in lib.moddit_last_error()
     rc = lib.moddit_sparsity_map(16, 16, 16, 16, 1, 1, 128, 64, s, s, 0.1, -1.0, 0, 0, 2, 32, 0, None)
     assert rc == _lib.MODDIT_EINVAL and b"block_size" in lib.moddit_last_error()
+    # the merged replay's lists must cover the video region's 128-row query tiles
+    rc = lib.moddit_sparsity_map_merge(16, 16, 16, 16, 1, 1, 256, 64, s, s, 0.1, -1.0, 0, 0, 4,
+                                       64, 0, 16, 16, 1, 4, None)
+    assert rc == _lib.MODDIT_EINVAL and b"needs 2" in lib.moddit_last_error()
+    rc = lib.moddit_sparsity_map_merge(16, 16, 16, 16, 1, 1, 256, 64, s, s, 0.1, -1.0, 0, 0, 4,
+                                       64, 0, None, None, 2, 4, None)
+    assert rc == _lib.MODDIT_EINVAL and b"tile lists" in lib.moddit_last_error()
     # the last map block must hold at least one token of the sequence
     rc = lib.moddit_sparsity_map(16, 16, 16, 16, 1, 1, 128, 64, s, s, 0.1, -1.0, 64, 64, 2, 64, 0,
                                  None)
