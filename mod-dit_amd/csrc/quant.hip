@@ -169,7 +169,6 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantParams p) {
   __shared__ float mean[D];
   __shared__ float vinv[D];
   __shared__ float wmax[4][3];  // per wave: Q block 0, Q block 1, K tile
-  __shared__ uint8_t vt[D][64 + 4];  // transposed fp8 V tile (+4: fewer bank conflicts)
   const int bh = blockIdx.x;
   const int tile = blockIdx.y;
   const int b = bh / p.heads;
@@ -199,20 +198,15 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantParams p) {
     const int c = idx % kChunks;
     const int s = row0 + r;
     const bool ok = s >= 0 && s < p.seq_len;
-    u32x4 qw = {0u, 0u, 0u, 0u}, kw = {0u, 0u, 0u, 0u}, vw = {0u, 0u, 0u, 0u};
+    u32x4 qw = {0u, 0u, 0u, 0u}, kw = {0u, 0u, 0u, 0u};
     if (ok) {
       qw = *reinterpret_cast<const u32x4*>(qb + s * p.q_ss + c * 8);
       kw = *reinterpret_cast<const u32x4*>(kb + s * p.k_ss + c * 8);
-      vw = *reinterpret_cast<const u32x4*>(vb + s * p.v_ss + c * 8);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       qv[i][j] = ok ? E::to_float(u16_at(qw, j)) : 0.f;
       kv[i][j] = ok ? E::to_float(u16_at(kw, j)) - mean[c * 8 + j] : 0.f;
-      const float vq = ok ? E::to_float(u16_at(vw, j)) * vinv[c * 8 + j] : 0.f;
-      // fp8 e4m3 (round to nearest even); padded keys are zero
-      const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(vq, 0.f, 0, false);
-      vt[c * 8 + j][r] = static_cast<uint8_t>(pk & 0xff);
       if (r < 32)
         qmax0 = fmaxf(qmax0, fabsf(qv[i][j]));
       else
@@ -275,15 +269,32 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantParams p) {
       *reinterpret_cast<u32x2*>(k8 + static_cast<int64_t>(s) * D + c * 8) = u32x2{kw[0], kw[1]};
     }
   }
-  // transposed fp8 V tile: row d, 64 grid columns (zeros outside the sequence)
+  // Transposed fp8 V tile, row d, 64 grid columns (zeros outside the sequence), without
+  // LDS: thread (g, c) loads keys 4g..4g+3 of the tile at channels 8c..8c+7 and packs the
+  // four keys of each channel into one word (e4m3, round to nearest even). Consecutive
+  // threads take consecutive key groups, so the 16 words of a channel row are 64
+  // contiguous bytes.
   uint8_t* vrow = p.v8t + (static_cast<int64_t>(bh) * D) * p.s_pad + tile * 64;
-  for (int e = tid; e < D * 16; e += kQThreads) {
-    const int d = e / 16;
-    const int c4 = e % 16;  // 4-byte group of keys
-    uint32_t w = 0;
+  for (int e = tid; e < 16 * kChunks; e += kQThreads) {
+    const int g = e % 16;  // group of 4 keys
+    const int c = e / 16;  // 16-byte chunk of channels
+    float vf[4][8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) w |= static_cast<uint32_t>(vt[d][c4 * 4 + t]) << (8 * t);
-    *reinterpret_cast<uint32_t*>(vrow + static_cast<int64_t>(d) * p.s_pad + c4 * 4) = w;
+    for (int t = 0; t < 4; ++t) {
+      const int s = row0 + 4 * g + t;
+      const bool ok = s >= 0 && s < p.seq_len;
+      u32x4 vw = {0u, 0u, 0u, 0u};
+      if (ok) vw = *reinterpret_cast<const u32x4*>(vb + s * p.v_ss + c * 8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vf[t][j] = ok ? E::to_float(u16_at(vw, j)) * vinv[c * 8 + j] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      int w = __builtin_amdgcn_cvt_pk_fp8_f32(vf[0][j], vf[1][j], 0, false);
+      w = __builtin_amdgcn_cvt_pk_fp8_f32(vf[2][j], vf[3][j], w, true);
+      *reinterpret_cast<uint32_t*>(vrow + static_cast<int64_t>(c * 8 + j) * p.s_pad + 4 * g) =
+          static_cast<uint32_t>(w);
+    }
   }
 }
 
