@@ -268,13 +268,18 @@ __global__ __launch_bounds__(kThreads, (kRagged && D == 128) ? 2 : 3) __attribut
       for (int i = 1; i < 16; ++i) mi = max(mi, s0[i]);
 #pragma unroll
       for (int i = 0; i < 16; ++i) mi = max(mi, s1[i]);
+      // exchanged as an integer: the conversion and the scale (sc > 0) are monotone, so
+      // this is the max of the scaled halves, without the float max's NaN canonicalising
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(mi, mi, false, false);
+        mi = max(static_cast<int>(sw[0]), static_cast<int>(sw[1]));
+      }
       mx = static_cast<float>(mi) * sc;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         f0[i] = static_cast<float>(s0[i]);
         f1[i] = static_cast<float>(s1[i]);
       }
-      mx = max_over_halves(mx);
       const bool need = mx > m_run + kRescaleSlack;
       rescale = __ballot(need) != 0ull;
       const float m_new = need ? mx : m_run;
@@ -347,9 +352,11 @@ __global__ __launch_bounds__(kThreads, (kRagged && D == 128) ? 2 : 3) __attribut
       const float b2 = __builtin_amdgcn_exp2f(f1[4 * w + 2]);
       const float b3 = __builtin_amdgcn_exp2f(f1[4 * w + 3]);
       rs += ((a0 + a1) + (a2 + a3)) + ((b0 + b1) + (b2 + b3));
-      int wa = __builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, 0, false);
+      // each packing writes one half of the word; the previous tile's P word (dead once
+      // its P.V MFMA has issued) supplies the other half, so no register is zeroed first
+      int wa = __builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, pb[w], false);
       wa = __builtin_amdgcn_cvt_pk_fp8_f32(a2, a3, wa, true);
-      int wb = __builtin_amdgcn_cvt_pk_fp8_f32(b0, b1, 0, false);
+      int wb = __builtin_amdgcn_cvt_pk_fp8_f32(b0, b1, pb[4 + w], false);
       wb = __builtin_amdgcn_cvt_pk_fp8_f32(b2, b3, wb, true);
       pb[w] = wa;
       pb[4 + w] = wb;
@@ -426,9 +433,7 @@ __global__ __launch_bounds__(kThreads, (kRagged && D == 128) ? 2 : 3) __attribut
       i32x16 s0, s1;
       qk(ks1, s0, s1);
       pv(vs, pb);
-      i32x8 pn;
-      softmax(s0, s1, kt1, pn, pend_alpha, pend);
-      pb = pn;
+      softmax(s0, s1, kt1, pb, pend_alpha, pend);  // P_{j+1} overwrites P_j after its MFMAs
     } else {
       if (act_cur) pv(vs, pb);
       if (act_next) {
