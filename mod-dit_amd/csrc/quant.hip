@@ -187,6 +187,22 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantParams p) {
   const uint16_t* kb = p.k + b * p.k_sb + h * p.k_sh;
   const uint16_t* vb = p.v + b * p.v_sb + h * p.v_sh;
   const int row0 = p.origin + tile * 64;  // token of the tile's first row
+
+  // V for the transposed fp8 tile (written last) is loaded first, so that its reads
+  // overlap the Q/K work: thread (g, c) = (tid % 16, tid / 16) takes keys 4g..4g+3 of the
+  // tile at channels 8c..8c+7 (tokens outside the sequence load as zero)
+  static_assert(16 * kChunks <= kQThreads, "one V group per thread");
+  const int vg = tid % 16;
+  const int vc = tid / 16;
+  const bool v_thread = vc < kChunks;
+  u32x4 vraw[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int s = row0 + 4 * vg + t;
+    vraw[t] = u32x4{0u, 0u, 0u, 0u};
+    if (v_thread && s >= 0 && s < p.seq_len)
+      vraw[t] = *reinterpret_cast<const u32x4*>(vb + s * p.v_ss + vc * 8);
+  }
   // thread chunk i covers row i*kQThreads/kChunks + tid/kChunks, 16-byte chunk tid%kChunks:
   // the kChunks threads of a row are consecutive lanes of one wave
   float qv[kPerThread][8], kv[kPerThread][8];
@@ -270,29 +286,25 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(QuantParams p) {
     }
   }
   // Transposed fp8 V tile, row d, 64 grid columns (zeros outside the sequence), without
-  // LDS: thread (g, c) loads keys 4g..4g+3 of the tile at channels 8c..8c+7 and packs the
-  // four keys of each channel into one word (e4m3, round to nearest even). Consecutive
-  // threads take consecutive key groups, so the 16 words of a channel row are 64
-  // contiguous bytes.
-  uint8_t* vrow = p.v8t + (static_cast<int64_t>(bh) * D) * p.s_pad + tile * 64;
-  for (int e = tid; e < 16 * kChunks; e += kQThreads) {
-    const int g = e % 16;  // group of 4 keys
-    const int c = e / 16;  // 16-byte chunk of channels
+  // LDS: thread (g, c) packs the four keys of each of its channels into one word (e4m3,
+  // round to nearest even). Consecutive threads take consecutive key groups, so the 16
+  // words of a channel row are 64 contiguous bytes.
+  if (v_thread) {
+    uint8_t* vrow = p.v8t + (static_cast<int64_t>(bh) * D) * p.s_pad + tile * 64;
     float vf[4][8];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int s = row0 + 4 * g + t;
+      const int s = row0 + 4 * vg + t;
       const bool ok = s >= 0 && s < p.seq_len;
-      u32x4 vw = {0u, 0u, 0u, 0u};
-      if (ok) vw = *reinterpret_cast<const u32x4*>(vb + s * p.v_ss + c * 8);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) vf[t][j] = ok ? E::to_float(u16_at(vw, j)) * vinv[c * 8 + j] : 0.f;
+      for (int j = 0; j < 8; ++j)
+        vf[t][j] = ok ? E::to_float(u16_at(vraw[t], j)) * vinv[vc * 8 + j] : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       int w = __builtin_amdgcn_cvt_pk_fp8_f32(vf[0][j], vf[1][j], 0, false);
       w = __builtin_amdgcn_cvt_pk_fp8_f32(vf[2][j], vf[3][j], w, true);
-      *reinterpret_cast<uint32_t*>(vrow + static_cast<int64_t>(c * 8 + j) * p.s_pad + 4 * g) =
+      *reinterpret_cast<uint32_t*>(vrow + static_cast<int64_t>(vc * 8 + j) * p.s_pad + 4 * vg) =
           static_cast<uint32_t>(w);
     }
   }
