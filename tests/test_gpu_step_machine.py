@@ -15,7 +15,7 @@ import torch
 import mod_dit_amd as md
 import oracle as O
 from mod_dit_amd import ops
-from q8_contract import check_q8_model
+from q8_contract import check_q8_exact, check_q8_model
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -271,6 +271,51 @@ def test_configs1_cogvideox_full_shape():
         kn, vn = _np(k[0, heads]), _np(v[0, heads])
         ref, _ = O.masked_attention(qn, kn, vn, tm, dtype=np.float64)
         _check_attn(out[0, heads][:, rows], ref, "cogvideox full-shape sparse", sparse=True)
+
+
+def test_configs1_cogvideox_full_shape_int8():
+    """The int8 Q.K^T / fp8 P.V engine (precision='int8', MoD/mod/attn_mask.py:306) on
+    the CogVideoX-sized layer of test_configs1_cogvideox_full_shape: head_dim 64, text
+    first, the grid shifted to the text blocks. Rows covering the text, the first video
+    block and the partial last one, for the first and last head, against exact fp64
+    attention on the unquantised inputs under the executed mask, elementwise within the
+    bound derived from the rounding model of that arithmetic (oracle.q8_exact_error_bound,
+    the same contract as the d=128 layers)."""
+    H, D, bs = 48, 64, 64
+    text, F, tpf = 226, 13, 1350
+    video = F * tpf
+    S = text + video
+    W, T, thr = 4, 3, 1e-4
+    tb, vb, origin = O.cogvideox_grid(text, video, bs)
+    top_k = round(0.25 * vb)
+    st = md.create_adaptive_mask_state("cogvideox", H, video, text, tpf, F, warmup_steps=W,
+                                       top_k=top_k, predict_T=T, threshold=thr, block_size=bs,
+                                       tile_rows="exact", precision="int8")
+    g = torch.Generator().manual_seed(2024)
+    rows = np.r_[0:300, S - 200:S]
+    checked = 0
+    for step in range(W + 1):
+        q, k, v = ((torch.randn(1, H, S, D, generator=g) * D ** -0.5).to(torch.bfloat16).to(DEV)
+                   for _ in range(3))
+        out, _ = md.SparseAttentionWithMap(q, k, v, st, None, current_step=step,
+                                           use_dense=step < W - 2)
+        if O.step_phase(step, W, T) != "sparse":
+            continue
+        torch.cuda.synchronize()
+        tiles = st["_tiles"]
+        assert tiles.origin == origin
+        qz = ops.quantize_qkv(q, k, v, grid_origin=tiles.origin)  # what the engine quantised
+        counts, entries = tiles.counts.cpu().numpy(), tiles.entries.cpu().numpy()
+        for h in (0, H - 1):
+            qh, kh, vh = (_np(t[0, h]).astype(np.float64) for t in (q, k, v))
+            tm = O.token_mask_rows_from_tiles(counts[h], entries[h], rows, S, origin=origin)
+            err, bound, E = check_q8_exact(_np(out[0, h])[rows], qh, kh, vh, qz, 0, h, rows, tm,
+                                           tag=f"cogvideox int8 head {h}")
+            print(f"cogvideox int8 head {h}: max-abs {err.max():.3e} mean-abs {err.mean():.3e}; "
+                  f"worst element at {(err / bound).max():.3f} of its bound; E median "
+                  f"{np.median(E):.3f}", flush=True)
+            checked += 1
+    assert checked == 2
 
 
 def test_use_dense_and_error_paths():
